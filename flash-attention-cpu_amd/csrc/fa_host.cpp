@@ -1,0 +1,507 @@
+// fa_host.cpp -- host side of libfa_hip.so: the C ABI declared in
+// include/fa_hip.h over the HIP runtime C API.
+//
+// Replaces the reference crate's entry / dispatch layer
+// (amaye15/flash-attention-cpu): check_shapes (src/common.rs:41-57), the
+// per-variant entry points (src/v1.rs:51-159, src/v2.rs:49-157,
+// src/v3.rs:61-169) and multihead_dispatch (src/common.rs:72-101).  The
+// crate's runtime ISA pick (src/v2.rs:63-120) becomes a pick among gfx950
+// kernel instantiations (padded d_head, 128-bit vs scalar loads, prefill vs
+// split-KV), and rayon's fan-out over (head, query block) becomes the
+// launch grid.
+//
+// Kernels live in a code object (fa_kernels.hsaco, built from
+// fa_kernels.hip) that is loaded once per device with hipModuleLoad and
+// launched with hipModuleLaunchKernel.  There is no CPU compute path.
+
+#include <dlfcn.h>
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "../../include/fa_hip.h"
+#include "fa_params.h"
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+constexpr int kMaxD = 256;
+constexpr int kPrefillRows = 128;   // query rows per prefill workgroup
+constexpr int kDecodeRows = 16;     // query rows per split-KV wave
+constexpr int kDecodeWaves = 4;     // waves per split-KV workgroup
+
+struct DeviceState {
+    std::once_flag once;
+    int status = FA_OK;
+    hipModule_t module = nullptr;
+    int num_cus = 256;
+    std::mutex fn_mu;
+    std::unordered_map<std::string, hipFunction_t> fns;
+    // Host-slice calls: one staging allocation and stream per device.
+    std::mutex io_mu;
+    hipStream_t io_stream = nullptr;
+    float* io_buf = nullptr;
+    size_t io_floats = 0;
+};
+
+DeviceState g_dev[kMaxDevices];
+
+std::string module_path() {
+    const char* env = std::getenv("FA_HIP_MODULE");
+    if (env && *env) return std::string(env);
+    Dl_info info;
+    if (dladdr(reinterpret_cast<void*>(&fa_init), &info) && info.dli_fname) {
+        std::string p(info.dli_fname);
+        const size_t pos = p.rfind('/');
+        const std::string dir = (pos == std::string::npos) ? std::string(".") : p.substr(0, pos);
+        return dir + "/fa_kernels.hsaco";
+    }
+    return "fa_kernels.hsaco";
+}
+
+int current_device(int* dev) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        return FA_ERR_NO_DEVICE;
+    }
+    if (hipGetDevice(dev) != hipSuccess || *dev < 0 || *dev >= kMaxDevices) return FA_ERR_NO_DEVICE;
+    return FA_OK;
+}
+
+int ensure_loaded(int dev) {
+    DeviceState& s = g_dev[dev];
+    std::call_once(s.once, [&] {
+        const std::string path = module_path();
+        if (FILE* f = std::fopen(path.c_str(), "rb")) {
+            std::fclose(f);
+        } else {
+            s.status = FA_ERR_MODULE;
+            return;
+        }
+        if (hipModuleLoad(&s.module, path.c_str()) != hipSuccess) {
+            (void)hipGetLastError();
+            s.status = FA_ERR_MODULE;
+            return;
+        }
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0)
+            s.num_cus = prop.multiProcessorCount;
+        s.status = FA_OK;
+    });
+    return s.status;
+}
+
+int get_function(int dev, const std::string& name, hipFunction_t* fn) {
+    DeviceState& s = g_dev[dev];
+    std::lock_guard<std::mutex> lock(s.fn_mu);
+    auto it = s.fns.find(name);
+    if (it != s.fns.end()) {
+        *fn = it->second;
+        return FA_OK;
+    }
+    hipFunction_t f = nullptr;
+    if (hipModuleGetFunction(&f, s.module, name.c_str()) != hipSuccess) {
+        (void)hipGetLastError();
+        return FA_ERR_MODULE;
+    }
+    s.fns.emplace(name, f);
+    *fn = f;
+    return FA_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Launch planning: which kernels, what grid, what workspace.
+// ---------------------------------------------------------------------------
+struct Launch {
+    std::string name;
+    unsigned gx = 1, gy = 1, gz = 1, bx = 1;
+};
+
+struct Plan {
+    bool split = false;
+    Launch first, second;   // second is the split-KV merge
+    FaParams p{};
+    size_t ws_floats = 0;   // split-KV workspace (part_o + part_ml)
+};
+
+int pad_d(size_t d) {
+    if (d <= 32) return 32;
+    if (d <= 64) return 64;
+    if (d <= 128) return 128;
+    return 256;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int make_plan(int variant, const float* q, const float* k, const float* v, const float* out,
+              size_t bh, size_t sq, size_t sk, size_t d, int causal, const fa_launch_opts* opts,
+              int num_cus, Plan* plan) {
+    if (variant < 1 || variant > 3) return FA_ERR_INVALID_ARG;
+    const int path = opts ? opts->path : FA_PATH_AUTO;
+    if (path < FA_PATH_AUTO || path > FA_PATH_SPLITKV) return FA_ERR_INVALID_ARG;
+    if (path == FA_PATH_SPLITKV && variant == 1) return FA_ERR_INVALID_ARG;
+    if (opts && opts->num_splits < 0) return FA_ERR_INVALID_ARG;
+    if (d > (size_t)kMaxD) return FA_ERR_UNSUPPORTED;
+    const size_t imax = 0x7fffffff;
+    if (sq > imax || sk > imax || bh > imax) return FA_ERR_UNSUPPORTED;
+
+    const int D = pad_d(d);
+    const bool vec = (d % 4 == 0) && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
+    float scale = 1.0f / std::sqrt(static_cast<float>(d));   // src/v2.rs:171
+    if (opts && opts->softmax_scale > 0.0f && std::isfinite(opts->softmax_scale)) scale = opts->softmax_scale;
+
+    FaParams& p = plan->p;
+    std::memset(&p, 0, sizeof(p));
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.out = const_cast<float*>(out);
+    p.bh = static_cast<int>(bh);
+    p.seq_q = static_cast<int>(sq);
+    p.seq_k = static_cast<int>(sk);
+    p.d = static_cast<int>(d);
+    p.causal = causal ? 1 : 0;
+    p.scale_log2e = scale * 1.44269504088896341f;
+
+    const size_t nqb = (sq + kPrefillRows - 1) / kPrefillRows;
+    const size_t nqt = (sq + kDecodeRows - 1) / kDecodeRows;
+    bool split = false;
+    if (variant != 1) {
+        if (path == FA_PATH_SPLITKV) {
+            split = true;
+        } else if (path == FA_PATH_AUTO) {
+            split = sq <= 64 && sk >= 512 && nqb * bh < (size_t)num_cus;
+        }
+    }
+    if (split && nqt * bh > 65535) {
+        if (path == FA_PATH_SPLITKV) return FA_ERR_UNSUPPORTED;
+        split = false;
+    }
+    plan->split = split;
+    char buf[64];
+    if (!split) {
+        if (nqb * bh > imax) return FA_ERR_UNSUPPORTED;
+        p.nqb = static_cast<int>(nqb);
+        // 0: scalar loads (any d), 1: 128-bit loads, 2: global->LDS DMA (v3)
+        const int loader = vec ? (variant == 3 ? 2 : 1) : 0;
+        std::snprintf(buf, sizeof(buf), "fa_prefill_v%d_d%d_%d", variant, D, loader);
+        plan->first.name = buf;
+        plan->first.gx = static_cast<unsigned>(nqb * bh);
+        plan->first.bx = 512;
+        plan->ws_floats = 0;
+        return FA_OK;
+    }
+    // Split-KV: each workgroup takes split_len keys (a multiple of 64) for one
+    // (bh, 16-row query tile); aim for ~4 workgroups per CU.
+    size_t nsplit;
+    if (opts && opts->num_splits > 0) {
+        nsplit = (size_t)opts->num_splits;
+    } else {
+        const size_t target = 4 * (size_t)num_cus;
+        nsplit = target / (nqt * bh);
+        if (nsplit < 1) nsplit = 1;
+    }
+    size_t split_len = (sk + nsplit - 1) / nsplit;
+    split_len = ((split_len + 63) / 64) * 64;
+    nsplit = (sk + split_len - 1) / split_len;
+    if (nsplit > imax || split_len > imax) return FA_ERR_UNSUPPORTED;
+    p.nqt = static_cast<int>(nqt);
+    p.num_splits = static_cast<int>(nsplit);
+    p.split_len = static_cast<int>(split_len);
+    std::snprintf(buf, sizeof(buf), "fa_decode_d%d_%d", D, vec ? 1 : 0);
+    plan->first.name = buf;
+    plan->first.gx = static_cast<unsigned>(nsplit);
+    plan->first.gy = static_cast<unsigned>(nqt);
+    plan->first.gz = static_cast<unsigned>(bh);
+    plan->first.bx = 64 * kDecodeWaves;
+    std::snprintf(buf, sizeof(buf), "fa_merge_d%d", D);
+    plan->second.name = buf;
+    const size_t threads = bh * sq * ((d + 3) / 4);
+    plan->second.gx = static_cast<unsigned>((threads + 255) / 256);
+    plan->second.bx = 256;
+    plan->ws_floats = bh * nqt * nsplit * (16 * (size_t)D + 32);
+    return FA_OK;
+}
+
+int launch(int dev, const Launch& L, FaParams* p, hipStream_t stream) {
+    hipFunction_t fn;
+    int rc = get_function(dev, L.name, &fn);
+    if (rc != FA_OK) return rc;
+    void* args[] = {p};
+    if (hipModuleLaunchKernel(fn, L.gx, L.gy, L.gz, L.bx, 1, 1, 0, stream, args, nullptr) != hipSuccess) {
+        (void)hipGetLastError();
+        return FA_ERR_LAUNCH;
+    }
+    return FA_OK;
+}
+
+// Queue one attention call on device pointers.
+int run_device(int variant, hipStream_t stream, const float* q, const float* k, const float* v, size_t bh,
+               size_t sq, size_t sk, size_t d, int causal, const fa_launch_opts* opts, float* out) {
+    if (bh == 0 || sq == 0 || sk == 0 || d == 0) return FA_OK;   // src/common.rs:56
+    if (!q || !k || !v || !out) return FA_ERR_INVALID_ARG;
+    int dev;
+    int rc = current_device(&dev);
+    if (rc != FA_OK) return rc;
+    rc = ensure_loaded(dev);
+    if (rc != FA_OK) return rc;
+    Plan plan;
+    rc = make_plan(variant, q, k, v, out, bh, sq, sk, d, causal, opts, g_dev[dev].num_cus, &plan);
+    if (rc != FA_OK) return rc;
+    if (!plan.split) return launch(dev, plan.first, &plan.p, stream);
+
+    float* ws = nullptr;
+    if (hipMallocAsync(reinterpret_cast<void**>(&ws), plan.ws_floats * sizeof(float), stream) != hipSuccess) {
+        (void)hipGetLastError();
+        return FA_ERR_ALLOC;
+    }
+    const int D = pad_d(d);
+    plan.p.part_o = ws;
+    plan.p.part_ml = ws + bh * (size_t)plan.p.nqt * plan.p.num_splits * 16 * D;
+    rc = launch(dev, plan.first, &plan.p, stream);
+    if (rc == FA_OK) rc = launch(dev, plan.second, &plan.p, stream);
+    if (hipFreeAsync(ws, stream) != hipSuccess) {
+        (void)hipGetLastError();
+        if (rc == FA_OK) rc = FA_ERR_ALLOC;
+    }
+    return rc;
+}
+
+int check_single(size_t q_len, size_t k_len, size_t v_len, size_t out_len, size_t sq, size_t sk,
+                 size_t d) {
+    if (q_len != sq * d) return FA_ERR_Q_SHAPE;
+    if (k_len != sk * d) return FA_ERR_K_SHAPE;
+    if (v_len != sk * d) return FA_ERR_V_SHAPE;
+    if (out_len != sq * d) return FA_ERR_OUT_SHAPE;
+    return FA_OK;
+}
+
+// Host slices: copy in, run, copy out, synchronise.  Serialised per device.
+int run_host(int variant, const float* q, const float* k, const float* v, size_t bh, size_t sq, size_t sk,
+             size_t d, const fa_config* cfg, float* out) {
+    if (bh == 0 || sq == 0 || sk == 0 || d == 0) return FA_OK;   // out untouched
+    if (!q || !k || !v || !out) return FA_ERR_INVALID_ARG;
+    const int causal = cfg ? cfg->causal : 0;
+    int dev;
+    int rc = current_device(&dev);
+    if (rc != FA_OK) return rc;
+    rc = ensure_loaded(dev);
+    if (rc != FA_OK) return rc;
+    DeviceState& s = g_dev[dev];
+    std::lock_guard<std::mutex> lock(s.io_mu);
+    if (!s.io_stream) {
+        if (hipStreamCreateWithFlags(&s.io_stream, hipStreamNonBlocking) != hipSuccess) {
+            (void)hipGetLastError();
+            s.io_stream = nullptr;
+            return FA_ERR_LAUNCH;
+        }
+    }
+    // 64-float alignment keeps every operand 256-byte aligned.
+    auto up = [](size_t n) { return (n + 63) / 64 * 64; };
+    const size_t nq = bh * sq * d, nk = bh * sk * d;
+    const size_t need = up(nq) * 2 + up(nk) * 2;
+    if (need > s.io_floats) {
+        if (s.io_buf) (void)hipFree(s.io_buf);
+        s.io_buf = nullptr;
+        s.io_floats = 0;
+        if (hipMalloc(reinterpret_cast<void**>(&s.io_buf), need * sizeof(float)) != hipSuccess) {
+            (void)hipGetLastError();
+            return FA_ERR_ALLOC;
+        }
+        s.io_floats = need;
+    }
+    float* dq = s.io_buf;
+    float* dk = dq + up(nq);
+    float* dv = dk + up(nk);
+    float* dout = dv + up(nk);
+    hipStream_t st = s.io_stream;
+    if (hipMemcpyAsync(dq, q, nq * sizeof(float), hipMemcpyHostToDevice, st) != hipSuccess ||
+        hipMemcpyAsync(dk, k, nk * sizeof(float), hipMemcpyHostToDevice, st) != hipSuccess ||
+        hipMemcpyAsync(dv, v, nk * sizeof(float), hipMemcpyHostToDevice, st) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipStreamSynchronize(st);
+        return FA_ERR_COPY;
+    }
+    rc = run_device(variant, st, dq, dk, dv, bh, sq, sk, d, causal, nullptr, dout);
+    if (rc != FA_OK) {
+        (void)hipStreamSynchronize(st);
+        return rc;
+    }
+    if (hipMemcpyAsync(out, dout, nq * sizeof(float), hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess) {
+        (void)hipGetLastError();
+        return FA_ERR_COPY;
+    }
+    return FA_OK;
+}
+
+int single(int variant, const float* q, size_t q_len, const float* k, size_t k_len, const float* v,
+           size_t v_len, size_t sq, size_t sk, size_t d, const fa_config* cfg, float* out, size_t out_len) {
+    const int rc = check_single(q_len, k_len, v_len, out_len, sq, sk, d);
+    if (rc != FA_OK) return rc;
+    return run_host(variant, q, k, v, 1, sq, sk, d, cfg, out);
+}
+
+int multi(int variant, const float* q, size_t q_len, const float* k, size_t k_len, const float* v,
+          size_t v_len, size_t batch, size_t heads, size_t sq, size_t sk, size_t d, const fa_config* cfg,
+          float* out, size_t out_len) {
+    // multihead_dispatch's totals (src/common.rs:85-90)
+    const size_t bh = batch * heads;
+    if (q_len != bh * sq * d) return FA_ERR_Q_SHAPE;
+    if (k_len != bh * sk * d) return FA_ERR_K_SHAPE;
+    if (v_len != bh * sk * d) return FA_ERR_V_SHAPE;
+    if (out_len != bh * sq * d) return FA_ERR_OUT_SHAPE;
+    return run_host(variant, q, k, v, bh, sq, sk, d, cfg, out);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+const char* fa_status_string(int status) {
+    switch (status) {
+        case FA_OK: return "ok";
+        case FA_ERR_Q_SHAPE: return "q shape mismatch";
+        case FA_ERR_K_SHAPE: return "k shape mismatch";
+        case FA_ERR_V_SHAPE: return "v shape mismatch";
+        case FA_ERR_OUT_SHAPE: return "out shape mismatch";
+        case FA_ERR_INVALID_ARG: return "invalid argument";
+        case FA_ERR_UNSUPPORTED: return "unsupported shape (d_head > 256 or size beyond 32-bit indexing)";
+        case FA_ERR_NO_DEVICE: return "no HIP device available";
+        case FA_ERR_MODULE: return "cannot load the gfx950 code object (fa_kernels.hsaco / FA_HIP_MODULE)";
+        case FA_ERR_ALLOC: return "device allocation failed";
+        case FA_ERR_LAUNCH: return "kernel launch failed";
+        case FA_ERR_COPY: return "host/device copy failed";
+        default: return "unknown status";
+    }
+}
+
+fa_config fa_config_default(void) {
+    fa_config c;
+    c.block_size_q = 64;
+    c.block_size_kv = 128;
+    c.causal = 0;
+    return c;
+}
+
+int fa_init(void) {
+    int dev;
+    const int rc = current_device(&dev);
+    if (rc != FA_OK) return rc;
+    return ensure_loaded(dev);
+}
+
+int fa_v1(const float* q, size_t q_len, const float* k, size_t k_len, const float* v, size_t v_len, size_t sq,
+          size_t sk, size_t d, const fa_config* cfg, float* out, size_t out_len) {
+    return single(1, q, q_len, k, k_len, v, v_len, sq, sk, d, cfg, out, out_len);
+}
+int fa_v2(const float* q, size_t q_len, const float* k, size_t k_len, const float* v, size_t v_len, size_t sq,
+          size_t sk, size_t d, const fa_config* cfg, float* out, size_t out_len) {
+    return single(2, q, q_len, k, k_len, v, v_len, sq, sk, d, cfg, out, out_len);
+}
+int fa_v3(const float* q, size_t q_len, const float* k, size_t k_len, const float* v, size_t v_len, size_t sq,
+          size_t sk, size_t d, const fa_config* cfg, float* out, size_t out_len) {
+    return single(3, q, q_len, k, k_len, v, v_len, sq, sk, d, cfg, out, out_len);
+}
+int fa_attention(const float* q, size_t q_len, const float* k, size_t k_len, const float* v, size_t v_len,
+                 size_t sq, size_t sk, size_t d, const fa_config* cfg, float* out, size_t out_len) {
+    return single(2, q, q_len, k, k_len, v, v_len, sq, sk, d, cfg, out, out_len);
+}
+
+int fa_multihead_v1(const float* q, size_t q_len, const float* k, size_t k_len, const float* v, size_t v_len,
+                    size_t batch, size_t heads, size_t sq, size_t sk, size_t d, const fa_config* cfg, float* out,
+                    size_t out_len) {
+    return multi(1, q, q_len, k, k_len, v, v_len, batch, heads, sq, sk, d, cfg, out, out_len);
+}
+int fa_multihead_v2(const float* q, size_t q_len, const float* k, size_t k_len, const float* v, size_t v_len,
+                    size_t batch, size_t heads, size_t sq, size_t sk, size_t d, const fa_config* cfg, float* out,
+                    size_t out_len) {
+    return multi(2, q, q_len, k, k_len, v, v_len, batch, heads, sq, sk, d, cfg, out, out_len);
+}
+int fa_multihead_v3(const float* q, size_t q_len, const float* k, size_t k_len, const float* v, size_t v_len,
+                    size_t batch, size_t heads, size_t sq, size_t sk, size_t d, const fa_config* cfg, float* out,
+                    size_t out_len) {
+    return multi(3, q, q_len, k, k_len, v, v_len, batch, heads, sq, sk, d, cfg, out, out_len);
+}
+int fa_attention_multihead(const float* q, size_t q_len, const float* k, size_t k_len, const float* v,
+                           size_t v_len, size_t batch, size_t heads, size_t sq, size_t sk, size_t d,
+                           const fa_config* cfg, float* out, size_t out_len) {
+    return multi(2, q, q_len, k, k_len, v, v_len, batch, heads, sq, sk, d, cfg, out, out_len);
+}
+
+int fa_device_v1(void* stream, const float* q, const float* k, const float* v, size_t batch, size_t heads,
+                 size_t sq, size_t sk, size_t d, const fa_config* cfg, float* out) {
+    return run_device(1, static_cast<hipStream_t>(stream), q, k, v, batch * heads, sq, sk, d,
+                      cfg ? cfg->causal : 0, nullptr, out);
+}
+int fa_device_v2(void* stream, const float* q, const float* k, const float* v, size_t batch, size_t heads,
+                 size_t sq, size_t sk, size_t d, const fa_config* cfg, float* out) {
+    return run_device(2, static_cast<hipStream_t>(stream), q, k, v, batch * heads, sq, sk, d,
+                      cfg ? cfg->causal : 0, nullptr, out);
+}
+int fa_device_v3(void* stream, const float* q, const float* k, const float* v, size_t batch, size_t heads,
+                 size_t sq, size_t sk, size_t d, const fa_config* cfg, float* out) {
+    return run_device(3, static_cast<hipStream_t>(stream), q, k, v, batch * heads, sq, sk, d,
+                      cfg ? cfg->causal : 0, nullptr, out);
+}
+
+int fa_device_ex(int variant, void* stream, const float* q, const float* k, const float* v, size_t batch,
+                 size_t heads, size_t sq, size_t sk, size_t d, const fa_config* cfg, const fa_launch_opts* opts,
+                 float* out) {
+    if (variant < 1 || variant > 3) return FA_ERR_INVALID_ARG;
+    return run_device(variant, static_cast<hipStream_t>(stream), q, k, v, batch * heads, sq, sk, d,
+                      cfg ? cfg->causal : 0, opts, out);
+}
+
+int fa_describe_launch(int variant, size_t batch, size_t heads, size_t sq, size_t sk, size_t d, int causal,
+                       const fa_launch_opts* opts, char* buf, size_t buf_len) {
+    int num_cus = 256;
+    int n = 0, dev = 0;
+    if (hipGetDeviceCount(&n) == hipSuccess && n > 0 && hipGetDevice(&dev) == hipSuccess) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0)
+            num_cus = prop.multiProcessorCount;
+    } else {
+        (void)hipGetLastError();
+    }
+    const size_t bh = batch * heads;
+    std::string text;
+    int rc = FA_OK;
+    if (bh == 0 || sq == 0 || sk == 0 || d == 0) {
+        text = "none";
+    } else {
+        Plan plan;
+        // Alignment is assumed (device allocations are 256-byte aligned).
+        static const float dummy[4] __attribute__((aligned(16))) = {0, 0, 0, 0};
+        rc = make_plan(variant, dummy, dummy, dummy, dummy, bh, sq, sk, d, causal, opts, num_cus, &plan);
+        if (rc == FA_OK) {
+            char tmp[256];
+            std::snprintf(tmp, sizeof(tmp), "%s grid=%ux%ux%u block=%u", plan.first.name.c_str(), plan.first.gx,
+                          plan.first.gy, plan.first.gz, plan.first.bx);
+            text = tmp;
+            if (plan.split) {
+                std::snprintf(tmp, sizeof(tmp), "; %s grid=%ux%ux%u block=%u; splits=%d split_len=%d",
+                              plan.second.name.c_str(), plan.second.gx, plan.second.gy, plan.second.gz,
+                              plan.second.bx, plan.p.num_splits, plan.p.split_len);
+                text += tmp;
+            }
+        }
+    }
+    if (buf && buf_len > 0) {
+        std::strncpy(buf, text.c_str(), buf_len - 1);
+        buf[buf_len - 1] = '\0';
+    }
+    return rc;
+}
+
+}  // extern "C"

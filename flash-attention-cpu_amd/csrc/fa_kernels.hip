@@ -1,0 +1,786 @@
+// fa_kernels.hip -- gfx950 (CDNA4) kernels for the FlashAttention forward pass.
+//
+// Replaces the reference crate's per-variant tiling loops and Kernel-trait
+// micro-kernels (amaye15/flash-attention-cpu):
+//   run_v1  src/v1.rs:162-396   -> fa_prefill<.., VARIANT=1, ..>
+//   run_v2  src/v2.rs:160-385   -> fa_prefill<.., VARIANT=2, ..>
+//   run_v3  src/v3.rs:351-512   -> fa_prefill<.., VARIANT=3, ..>
+//   dot4x4 / dot4 / dot         -> QK^T on v_mfma_f32_32x32x2_f32
+//   max_reduce4 / sub_exp_sum4  -> per-lane max/exp2/sum + v_permlane32_swap
+//   pv4 / axpy / scale_inplace  -> PV on v_mfma_f32_32x32x2_f32, per-lane rescale
+//   (new) split-KV + LSE merge  -> fa_decode / fa_merge for short-query shapes
+//
+// All arithmetic is IEEE f32 (f32 MFMA, no reduced-precision inputs).
+//
+// Prefill geometry (D = d_head padded to 32/64/128/256):
+//   * one workgroup owns BQ = 128 query rows of one (batch*head) slice;
+//     wave w owns rows 32*(w%4) .. +32 of that block;
+//   * keys are processed in wave tiles of 32; with KSPLIT = 2 (D <= 128) a
+//     workgroup has 8 waves and wave w takes the tiles of parity w/4, so every
+//     SIMD runs two waves on the same rows (one hides the other's softmax);
+//     the two partial (m, l, O) are merged through LDS at the end;
+//   * a stage of KSPLIT*32 keys of K and V sits in LDS, rows padded to D+4
+//     floats (conflict-free 128-bit reads);
+//   * scores are computed transposed, S^T = K Q^T (A = K rows from LDS, B = Q
+//     held in VGPRs), so each lane owns one query row and 16 of the tile's
+//     keys; its partner lane (lane ^ 32) owns the other 16;
+//   * the exp'd scores are then already the B operand of O^T = V^T P^T, and
+//     each lane's O^T accumulators belong to its own query row, so the
+//     online-softmax rescale is a per-lane multiply;
+//   * V is read with one 128-bit LDS read per MFMA step: lane i of a half
+//     reads V[key][NB*i .. NB*i+NB-1]; accumulator block j holds dv = NB*i+j.
+//
+// MFMA operand layouts (verified on MI355X):
+//   32x32x2 f32: A[i][k] in lane (i + 32k), B[k][j] in lane (j + 32k),
+//                C[i][j] in lane (j + 32*((i/4)%2)), reg 4*(i/8) + i%4.
+//   16x16x4 f32: A[i][k] in lane (i + 16k), B[k][j] in lane (j + 16k),
+//                C[i][j] in lane (j + 16*(i/4)), reg i%4.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "fa_params.h"
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+#define FA_NEG_INF (-__builtin_huge_valf())
+
+// ---------------------------------------------------------------------------
+// Small device helpers
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float fa_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// exp(a - b) in the log2 domain for running maxima that may still be -inf
+// (a row that has not seen a visible key yet): returns 0 when a == -inf.
+__device__ __forceinline__ float rescale_factor(float m_old, float m_new, float c) {
+    return (m_old == FA_NEG_INF) ? 0.0f : fa_exp2((m_old - m_new) * c);
+}
+
+template <bool VEC>
+__device__ __forceinline__ f32x4 load4(const float* __restrict__ base, int row, int nrows, int col, int d) {
+    f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (row < nrows) {
+        const float* p = base + (size_t)row * d + col;
+        if (VEC) {
+            if (col < d) v = *reinterpret_cast<const f32x4*>(p);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (col + e < d) v[e] = p[e];
+        }
+    }
+    return v;
+}
+
+// Workgroup -> (query block, batch*head) with the longest causal blocks first
+// (greedy longest-processing-time order as workgroups retire) and, when bh is
+// a multiple of 8, all blocks of one head on the same XCD (workgroups are
+// dispatched round-robin over the 8 XCDs) so its K/V stays in one L2.
+__device__ __forceinline__ void map_block(const FaParams& p, int& qb, int& bh) {
+    const int x = blockIdx.x;
+    int rank;
+    if (p.bh % 8 == 0) {
+        const int hpx = p.bh / 8;
+        const int xcd = x % 8, s = x / 8;
+        bh = (s % hpx) * 8 + xcd;
+        rank = s / hpx;
+    } else {
+        bh = x % p.bh;
+        rank = x / p.bh;
+    }
+    qb = p.causal ? (p.nqb - 1 - rank) : rank;
+}
+
+// ---------------------------------------------------------------------------
+// Prefill kernel: one template for v1 / v2 / v3.
+//
+// A workgroup of 8 waves owns BQ = 128 query rows of one (batch*head)
+// slice; wave w owns rows 16w .. 16w+15.  Keys stream through LDS in stages
+// of SK keys (64 for d <= 128, 32 for d = 256) shared by all 8 waves.
+//
+// Scores are computed transposed on 16x16x4 f32 MFMA, S^T = K Q^T: A = 16 K
+// rows from LDS, B = the wave's 16 Q rows held in VGPRs.  Lane l then owns
+// query row l%16 and keys 4*(l/16)+r (r = 0..3) of every 16-key block, so a
+// row's max / sum spans the 4 lanes l%16 + 16k (two swaps).  The exp'd
+// scores are already the B operand of O^T = V^T P^T, and lane l's O^T
+// accumulators all belong to its own query row, so the online-softmax
+// rescale is a per-lane multiply.  V is read with one 128-bit LDS read per
+// 64 output columns: lane l reads V[key][64hh + 4(l%16) .. +3], so O^T block
+// (hh, j) row i holds dv = 64hh + 4i + j.
+//
+// LDS holds K and V stages as rows of D + 4 floats: the 16-byte pad shifts
+// consecutive rows by 4 banks, so the row-per-lane K reads and the
+// contiguous V reads are conflict-free, and every read address is a
+// per-lane base plus an immediate offset.  The gfx950 global->LDS DMA
+// writes 1 KB runs of this padded image; pad slots re-load a valid chunk.
+//
+// LOADER: 0 = scalar global loads through VGPRs (any d), 1 = 128-bit loads
+// through VGPRs (d % 4 == 0), 2 = global_load_lds_dwordx4 DMA (d % 4 == 0,
+// 16-byte aligned operands; v3 only).
+// ---------------------------------------------------------------------------
+template <int D>
+__device__ __forceinline__ int lds_off(int row, int chunk) {
+    return row * (D + 4) + 4 * chunk;
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    // s_waitcnt with vmcnt = N and expcnt / lgkmcnt left at their maxima.
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// max / sum over the 4 lanes (l%16 + 16k) that hold one query row.  Both
+// swaps hand every lane the pair in the same order, so all 4 lanes end
+// with bit-identical results.
+__device__ __forceinline__ float row4_max(float x) {
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float row4_sum(float x) {
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+template <int D, int VARIANT, int LOADER>
+__device__ __forceinline__ void prefill_body(const FaParams& p) {
+    constexpr int NW = 8;                     // waves per workgroup
+    constexpr int NT = NW * 64;               // threads
+    constexpr int BQ = 128;                   // query rows per workgroup
+    constexpr int SK = (D <= 128) ? 64 : 32;  // keys per LDS stage
+    constexpr int KB = SK / 16;               // 16-key blocks per stage
+    constexpr int NQ = D / 4;                 // MFMA k-steps over d
+    constexpr int NC = D / 16;                // 128-bit K reads per lane per key block
+    constexpr int VW = (D >= 64) ? 4 : 2;     // floats per lane per V read
+    constexpr int NVR = (D >= 64) ? D / 64 : 1;   // V reads per key
+    constexpr int NOB = D / 16;               // O^T accumulator blocks
+    constexpr int CPR = D / 4;                // 16-byte chunks per row
+    constexpr int LDK = D + 4;                // padded LDS row (floats)
+    constexpr int TILE = SK * LDK;            // floats per K (or V) stage
+    constexpr bool DMA = (LOADER == 2);
+    constexpr int NBUF = (VARIANT == 3) ? 2 : 1;
+    static_assert(NVR * VW == NOB, "V read layout");
+    static_assert(!DMA || VARIANT == 3, "LDS DMA needs the double-buffered pipeline");
+    static_assert((SK * CPR) % NT == 0, "stage load must split evenly");
+
+    // Separate arrays so the compiler can tell a DMA in flight into one
+    // buffer from LDS reads of another (no needless vmcnt waits).
+    __shared__ __attribute__((aligned(16))) float Kb0[TILE];
+    __shared__ __attribute__((aligned(16))) float Vb0[TILE];
+    __shared__ __attribute__((aligned(16))) float Kb1[NBUF > 1 ? TILE : 4];
+    __shared__ __attribute__((aligned(16))) float Vb1[NBUF > 1 ? TILE : 4];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4;                  // lane group 0..3
+    const int li = lane & 15;
+
+    int qb, bh;
+    map_block(p, qb, bh);
+    const int seq_q = p.seq_q, seq_k = p.seq_k, d = p.d;
+    const int q0 = qb * BQ;
+    const float* __restrict__ Qh = p.q + (size_t)bh * seq_q * d;
+    const float* __restrict__ Kh = p.k + (size_t)bh * seq_k * d;
+    const float* __restrict__ Vh = p.v + (size_t)bh * seq_k * d;
+    float* __restrict__ Oh = p.out + (size_t)bh * seq_q * d;
+    const float c = p.scale_log2e;
+    const bool causal = p.causal != 0;
+
+    // Q rows of this wave as the B operand: lane holds Q[row][16cc + 4g + i].
+    const int row_first = q0 + 16 * wave;
+    const int qrow = row_first + li;
+    float qreg[NQ];
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) {
+        const f32x4 t = load4<LOADER != 0>(Qh, qrow, seq_q, 16 * cc + 4 * g, d);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qreg[4 * cc + i] = t[i];
+    }
+
+    f32x4 o[NOB];
+#pragma unroll
+    for (int j = 0; j < NOB; ++j) o[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    float m = FA_NEG_INF;   // running max of raw scores q.k (same in the row's 4 lanes)
+    float l = 0.0f;         // v2/v3: this lane's partial row sum; v1: full row sum
+
+    // Keys this workgroup visits: v1 visits every key (no causal skip,
+    // src/v1.rs:209-216); v2/v3 stop after the block's last diagonal key
+    // (src/v2.rs:208-212, src/v3.rs:396-410).
+    int kend = seq_k;
+    if (VARIANT != 1 && causal) kend = min(seq_k, q0 + BQ);
+    const int nst = (kend + SK - 1) / SK;
+
+    // ---- stage loaders ------------------------------------------------------
+    constexpr int LOAD_ITERS = (SK * CPR) / NT;
+    auto load_regs = [&](const float* __restrict__ src, int kbase, f32x4* rg) {
+#pragma unroll
+        for (int it = 0; it < LOAD_ITERS; ++it) {
+            const int idx = tid + it * NT;
+            rg[it] = load4<LOADER != 0>(src, kbase + idx / CPR, seq_k, 4 * (idx % CPR), d);
+        }
+    };
+    auto store_regs = [&](float* dst, const f32x4* rg) {
+#pragma unroll
+        for (int it = 0; it < LOAD_ITERS; ++it) {
+            const int idx = tid + it * NT;
+            *reinterpret_cast<f32x4*>(dst + lds_off<D>(idx / CPR, idx % CPR)) = rg[it];
+        }
+    };
+    // DMA: the stage image is SK rows of CPR + 1 chunks (the last one is the
+    // pad); run R = i*NW + w (64 chunks = 1 KB) is written by wave w, lane L
+    // fetching the global chunk that belongs at image position 64R + L.
+    // Rows past seq_k are clamped to a real row (masked to -inf / multiplied
+    // by 0 later), columns past d and pad slots to column 0, so every read
+    // is in bounds.
+    auto dma_stage = [&](const float* __restrict__ src, int kbase, float* dst) {
+        constexpr int TOTAL = SK * (CPR + 1);
+        constexpr int RUNS = (TOTAL + 63) / 64;
+        constexpr int NI = (RUNS + NW - 1) / NW;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int run = i * NW + wave;
+            if (run < RUNS) {
+                const int pos = run * 64 + lane;
+                const int r = pos / (CPR + 1), cidx = pos % (CPR + 1);
+                const int key = min(kbase + r, seq_k - 1);
+                const int col = (cidx < CPR && 4 * cidx < d) ? 4 * cidx : 0;
+                if (pos < TOTAL)
+                    __builtin_amdgcn_global_load_lds(src + (size_t)key * d + col, dst + run * 256, 16, 0, 0);
+            }
+        }
+    };
+    auto fill_stage = [&](const float* __restrict__ src, int kbase, float* dst) {
+        if constexpr (DMA) {
+            dma_stage(src, kbase, dst);
+        } else {
+            f32x4 rg[LOAD_ITERS];
+            load_regs(src, kbase, rg);
+            store_regs(dst, rg);
+        }
+    };
+
+    // ---- stage math ---------------------------------------------------------
+    // S^T for the stage's KB key blocks from `Ks`.  Blocked summation over
+    // d: each 128-bit K read feeds a fresh 4-step (16-product) MFMA chain
+    // whose result is then added to the running sum.  One long MFMA chain
+    // rounds like a sequential FMA loop; blocks of 16 bring the error down to
+    // that of the crate's 16-lane AVX-512 dot products (src/avx512.rs:195-234),
+    // which matters for large logits.
+    auto qk_stage = [&](const float* Ks, f32x4* s) {
+        // K operands one chunk ahead; a scheduling barrier per chunk keeps
+        // the live set to two chunks' reads.
+        f32x4 kk[2][KB];
+#pragma unroll
+        for (int b = 0; b < KB; ++b) kk[0][b] = *reinterpret_cast<const f32x4*>(Ks + lds_off<D>(16 * b + li, g));
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) {
+            if (cc + 1 < NC) {
+#pragma unroll
+                for (int b = 0; b < KB; ++b)
+                    kk[(cc + 1) & 1][b] =
+                        *reinterpret_cast<const f32x4*>(Ks + lds_off<D>(16 * b + li, 4 * (cc + 1) + g));
+            }
+#pragma unroll
+            for (int b = 0; b < KB; ++b) {
+                f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    t = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[cc & 1][b][i], qreg[4 * cc + i], t, 0, 0, 0);
+                s[b] = (cc == 0) ? t : s[b] + t;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // Mask keys >= seq_k and, when causal, keys > query row (top-left
+    // aligned, src/naive.rs:37; diagonal stages only, src/v2.rs:268-287).
+    auto mask_stage = [&](f32x4* s, int kbase) {
+        const bool need = (kbase + SK > seq_k) || (causal && kbase + SK - 1 > row_first);
+        if (need) {
+#pragma unroll
+            for (int b = 0; b < KB; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = kbase + 16 * b + 4 * g + r;
+                    if (key >= seq_k || (causal && key > qrow)) s[b][r] = FA_NEG_INF;
+                }
+        }
+    };
+
+    // Online-softmax update + PV for one stage (src/v2.rs:289-372; v1's
+    // normalise / un-normalise round trip, src/v1.rs:291-385).
+    auto softmax_pv = [&](f32x4* s, const float* Vs) {
+        float mt = s[0][0];
+#pragma unroll
+        for (int b = 0; b < KB; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mt = fmaxf(mt, s[b][r]);
+        mt = row4_max(mt);
+        const float m_new = fmaxf(m, mt);
+        const float m_use = (m_new == FA_NEG_INF) ? 0.0f : m_new;
+        // (s - m) is exact-rounded and <= 0, so the row maximum maps to
+        // exp2(0) = 1 exactly whatever the magnitude of the scores.
+        float ps = 0.0f;
+#pragma unroll
+        for (int b = 0; b < KB; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                s[b][r] = fa_exp2((s[b][r] - m_use) * c);
+                ps += s[b][r];
+            }
+        const float corr = rescale_factor(m, m_use, c);
+        m = m_new;
+        if (VARIANT == 1) {
+            const float l_new = corr * l + row4_sum(ps);
+            const float f = l * corr;
+#pragma unroll
+            for (int j = 0; j < NOB; ++j) o[j] *= f;
+            l = l_new;
+        } else {
+            l = corr * l + ps;
+#pragma unroll
+            for (int j = 0; j < NOB; ++j) o[j] *= corr;
+        }
+        // O^T += V^T P^T: 4 keys per MFMA step (key 16b + 4g + r in lane group
+        // g).  V operands one step ahead, a scheduling barrier per step.
+        auto read_v = [&](int step, f32x4* vv) {
+            const int kr = 16 * (step / 4) + 4 * g + (step % 4);
+#pragma unroll
+            for (int hh = 0; hh < NVR; ++hh) {
+                if constexpr (VW == 4) {
+                    vv[hh] = *reinterpret_cast<const f32x4*>(Vs + lds_off<D>(kr, 16 * hh + li));
+                } else {
+                    const f32x2 t = *reinterpret_cast<const f32x2*>(Vs + lds_off<D>(kr, li >> 1) + 2 * (li & 1));
+                    vv[hh] = (f32x4){t[0], t[1], 0.0f, 0.0f};
+                }
+            }
+        };
+        constexpr int VBUF = (NVR > 2) ? 1 : 2;   // d = 256: no read-ahead (registers)
+        f32x4 vv[VBUF][NVR];
+        if (VBUF > 1) {
+            read_v(0, vv[0]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int step = 0; step < 4 * KB; ++step) {
+            if (VBUF == 1) read_v(step, vv[0]);
+            else if (step + 1 < 4 * KB) read_v(step + 1, vv[(step + 1) % VBUF]);
+            const float pr = s[step / 4][step % 4];
+#pragma unroll
+            for (int hh = 0; hh < NVR; ++hh)
+#pragma unroll
+                for (int j = 0; j < VW; ++j)
+                    o[VW * hh + j] =
+                        __builtin_amdgcn_mfma_f32_16x16x4f32(vv[step % VBUF][hh][j], pr, o[VW * hh + j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (VARIANT == 1) {
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+            for (int j = 0; j < NOB; ++j) o[j] *= inv;
+        }
+    };
+
+    // Is this wave's share of stage `st` worth computing?  v2/v3 skip stages
+    // entirely in the future of every row of the wave; v1 does not.
+    auto stage_active = [&](int st) -> bool {
+        const int kbase = st * SK;
+        if (kbase >= seq_k) return false;
+        if (VARIANT != 1 && causal && kbase > row_first + 15) return false;
+        return true;
+    };
+
+    if constexpr (VARIANT == 3) {
+        // Double-buffered K and V (src/v3.rs:445-483: the next tile's scores
+        // are issued before the current tile is finished).  At step st, K(st+2)
+        // and V(st+1) stream by DMA into the buffers freed by the previous
+        // step while this step computes from resident data; stage st+1's QK^T
+        // is issued right after stage st's softmax + PV, and one barrier
+        // closes the step.  The loop is unrolled by two so every buffer is a
+        // compile-time choice.
+        fill_stage(Kh, 0, Kb0);
+        if (nst > 1) fill_stage(Kh, SK, Kb1);
+        fill_stage(Vh, 0, Vb0);
+        wait_vmcnt<0>();
+        __syncthreads();
+        f32x4 s_cur[KB];
+        bool act_cur = nst > 0 && stage_active(0);
+        if (act_cur) {
+            qk_stage(Kb0, s_cur);
+            mask_stage(s_cur, 0);
+        }
+        __syncthreads();   // Kb0 free for K(2)
+        auto step = [&](auto parity, int st) {
+            constexpr int P = decltype(parity)::value;
+            float* k_fill = P ? Kb1 : Kb0;        // K(st+2) -> buffer of K(st)
+            float* v_fill = P ? Vb0 : Vb1;        // V(st+1)
+            const float* k_next = P ? Kb0 : Kb1;  // K(st+1)
+            const float* v_cur = P ? Vb1 : Vb0;   // V(st)
+            const bool has_next = st + 1 < nst;
+            if (st + 2 < nst) fill_stage(Kh, (st + 2) * SK, k_fill);
+            if (has_next) fill_stage(Vh, (st + 1) * SK, v_fill);
+            const bool act_nxt = has_next && stage_active(st + 1);
+            // This stage's softmax + PV, then the next stage's QK^T from the
+            // other buffer, with no barrier between them: the second wave on
+            // each SIMD runs one while this wave runs the other.
+            if (act_cur) softmax_pv(s_cur, v_cur);
+            if (act_nxt) {
+                qk_stage(k_next, s_cur);
+                mask_stage(s_cur, (st + 1) * SK);
+            }
+            wait_vmcnt<0>();
+            __syncthreads();
+            act_cur = act_nxt;
+        };
+        for (int st = 0; st < nst; st += 2) {
+            step(std::integral_constant<int, 0>{}, st);
+            if (st + 1 < nst) step(std::integral_constant<int, 1>{}, st + 1);
+        }
+    } else {
+        // Single LDS stage; the next stage's global loads are issued into
+        // registers before the current stage computes.
+        f32x4 kr[LOAD_ITERS], vr[LOAD_ITERS];
+        if (nst > 0) {
+            load_regs(Kh, 0, kr);
+            load_regs(Vh, 0, vr);
+        }
+        for (int st = 0; st < nst; ++st) {
+            store_regs(Kb0, kr);
+            store_regs(Vb0, vr);
+            __syncthreads();
+            if (st + 1 < nst) {
+                load_regs(Kh, (st + 1) * SK, kr);
+                load_regs(Vh, (st + 1) * SK, vr);
+            }
+            if (stage_active(st)) {
+                f32x4 s[KB];
+                qk_stage(Kb0, s);
+                mask_stage(s, st * SK);
+                softmax_pv(s, Vb0);
+            }
+            __syncthreads();
+        }
+    }
+
+    // Final normalisation with the l > 0 guard (src/v2.rs:375-382; v1's
+    // accumulator is already normalised, src/v1.rs:389-393).
+    float inv = 1.0f;
+    if (VARIANT != 1) {
+        const float lt = row4_sum(l);
+        inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    }
+    if (qrow < seq_q) {
+        float* orow = Oh + (size_t)qrow * d;
+#pragma unroll
+        for (int hh = 0; hh < NVR; ++hh)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int dv0 = 64 * hh + VW * (4 * g + r);
+                if (LOADER != 0 && dv0 + VW <= d) {
+                    if constexpr (VW == 4) {
+                        const f32x4 t = {o[4 * hh][r] * inv, o[4 * hh + 1][r] * inv, o[4 * hh + 2][r] * inv,
+                                         o[4 * hh + 3][r] * inv};
+                        *reinterpret_cast<f32x4*>(orow + dv0) = t;
+                    } else {
+                        const f32x2 t = {o[0][r] * inv, o[1][r] * inv};
+                        *reinterpret_cast<f32x2*>(orow + dv0) = t;
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < VW; ++j)
+                        if (dv0 + j < d) orow[dv0 + j] = o[VW * hh + j][r] * inv;
+                }
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Split-KV decode kernel (new; no counterpart in the reference).
+//
+// For short query blocks against long key ranges: each wave takes 16 query
+// rows (zero-padded) and a contiguous key range of its split, computes
+// S^T = K Q^T on 16x16x4 MFMA straight from global memory (K and V are each
+// read once, with 128-bit loads), keeps (m, l, O) per query row, and the 4
+// waves of a workgroup merge through LDS into one partial per workgroup.
+// fa_merge then combines the partials of all splits by log-sum-exp.
+// ---------------------------------------------------------------------------
+template <int D, bool VEC>
+__device__ __forceinline__ void decode_body(const FaParams& p) {
+    constexpr int NQ = D / 4;          // MFMA k-steps over d (16x16x4)
+    constexpr int NKL = D / 16;        // 128-bit K loads per lane per 16 keys
+    constexpr int NVL = D / 64 > 0 ? D / 64 : 1;  // 128-bit V loads per lane per key step
+    constexpr int VW = D >= 64 ? 4 : D / 16;      // floats per lane per V load
+    constexpr int NOB = D / 16;        // O^T blocks of 16 dv
+    __shared__ __attribute__((aligned(16))) float lds[4 * (NOB * 4 * 64 + 128)];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lg = lane >> 4;          // lane group 0..3
+    const int lr = lane & 15;
+
+    const int split = blockIdx.x;
+    const int qt = blockIdx.y;
+    const int bh = blockIdx.z;
+    const int seq_q = p.seq_q, seq_k = p.seq_k, d = p.d;
+    const float* __restrict__ Qh = p.q + (size_t)bh * seq_q * d;
+    const float* __restrict__ Kh = p.k + (size_t)bh * seq_k * d;
+    const float* __restrict__ Vh = p.v + (size_t)bh * seq_k * d;
+    const float c = p.scale_log2e;
+    const bool causal = p.causal != 0;
+
+    const int q0 = qt * 16;
+    const int qrow = q0 + lr;          // this lane's query (score column)
+    const int qlast = min(seq_q, q0 + 16) - 1;
+
+    // This wave's keys.
+    const int k_split0 = split * p.split_len;
+    const int wave_len = p.split_len / 4;
+    int kbeg = k_split0 + wave * wave_len;
+    int kend = min(seq_k, kbeg + wave_len);
+    if (causal) kend = min(kend, qlast + 1);
+
+    // Q as the B operand: lane holds Q[qrow][16cc + 4lg + i] at qreg[4cc + i].
+    float qreg[NQ];
+#pragma unroll
+    for (int cc = 0; cc < D / 16; ++cc) {
+        f32x4 t = load4<VEC>(Qh, qrow, seq_q, 16 * cc + 4 * lg, d);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qreg[4 * cc + i] = t[i];
+    }
+
+    f32x4 o[NOB];
+#pragma unroll
+    for (int j = 0; j < NOB; ++j) o[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    float m = FA_NEG_INF, l = 0.0f;
+
+    // One 16-key block: K rows kb + lr (A operand), V rows kb + 4lg + r.
+    auto load_block = [&](int kb, f32x4* kk, f32x4* vv) {
+#pragma unroll
+        for (int cc = 0; cc < NKL; ++cc) kk[cc] = load4<VEC>(Kh, kb + lr, kend, 16 * cc + 4 * lg, d);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int hh = 0; hh < NVL; ++hh) {
+                if constexpr (VW == 4) {
+                    vv[r * NVL + hh] = load4<VEC>(Vh, kb + 4 * lg + r, kend, 64 * hh + 4 * lr, d);
+                } else {
+                    // D = 32: 2 floats per lane (dv = 2*lr + j)
+                    f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
+                    const int key = kb + 4 * lg + r;
+                    if (key < kend) {
+                        const float* vp = Vh + (size_t)key * d + VW * lr;
+#pragma unroll
+                        for (int e = 0; e < VW; ++e)
+                            if (VW * lr + e < d) t[e] = vp[e];
+                    }
+                    vv[r * NVL + hh] = t;
+                }
+            }
+    };
+    auto compute_block = [&](int kb, const f32x4* kk, const f32x4* vv) {
+        // Blocked summation over d, 16 products (4 MFMA steps) per block.
+        f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int cc = 0; cc < NKL; ++cc) {
+            f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                t = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[cc][i], qreg[4 * cc + i], t, 0, 0, 0);
+            s = (cc == 0) ? t : s + t;
+        }
+        // s[r] = score(key kb + 4lg + r, query qrow)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int key = kb + 4 * lg + r;
+            if (key >= kend || (causal && key > qrow)) s[r] = FA_NEG_INF;
+        }
+        float mt = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float m_new = fmaxf(m, mt);
+        const float m_use = (m_new == FA_NEG_INF) ? 0.0f : m_new;
+        float ps = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            s[r] = fa_exp2((s[r] - m_use) * c);
+            ps += s[r];
+        }
+        const float corr = rescale_factor(m, m_use, c);
+        m = m_new;
+        l = corr * l + ps;
+#pragma unroll
+        for (int j = 0; j < NOB; ++j) o[j] *= corr;
+        // O^T[dv][q] += V^T P^T: block (hh, j) row i <-> dv = 64hh + VW*i + j
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int hh = 0; hh < NVL; ++hh)
+#pragma unroll
+                for (int j = 0; j < VW; ++j)
+                    o[hh * VW + j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[r * NVL + hh][j], s[r],
+                                                                         o[hh * VW + j], 0, 0, 0);
+    };
+
+    f32x4 ka[NKL], va[4 * NVL], kb_[NKL], vb_[4 * NVL];
+    int kb = kbeg;
+    if (kb < kend) load_block(kb, ka, va);
+    while (kb < kend) {
+        const int kn = kb + 16;
+        if (kn < kend) load_block(kn, kb_, vb_);
+        compute_block(kb, ka, va);
+        kb = kn;
+        if (kb >= kend) break;
+        const int kn2 = kb + 16;
+        if (kn2 < kend) load_block(kn2, ka, va);
+        compute_block(kb, kb_, vb_);
+        kb = kn2;
+    }
+
+    // Row sums over the 4 lane groups.
+    l = l + __shfl_xor(l, 16);
+    l = l + __shfl_xor(l, 32);
+
+    // Merge the 4 waves through LDS: wave w writes, wave 0 combines.
+    float* mb = lds;
+    constexpr int WSTRIDE = NOB * 4 * 64 + 128;
+    if (wave != 0) {
+        float* w = mb + (wave - 1) * WSTRIDE;
+#pragma unroll
+        for (int j = 0; j < NOB; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) w[(j * 4 + r) * 64 + lane] = o[j][r];
+        w[NOB * 4 * 64 + lane] = m;
+        w[NOB * 4 * 64 + 64 + lane] = l;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    float mw[3];
+    float mn = m;
+#pragma unroll
+    for (int w = 0; w < 3; ++w) {
+        mw[w] = mb[w * WSTRIDE + NOB * 4 * 64 + lane];
+        mn = fmaxf(mn, mw[w]);
+    }
+    const float mu = (mn == FA_NEG_INF) ? 0.0f : mn;
+    const float c0 = rescale_factor(m, mu, c);
+    l *= c0;
+#pragma unroll
+    for (int j = 0; j < NOB; ++j) o[j] *= c0;
+#pragma unroll
+    for (int w = 0; w < 3; ++w) {
+        const float cw = rescale_factor(mw[w], mu, c);
+        l += mb[w * WSTRIDE + NOB * 4 * 64 + 64 + lane] * cw;
+#pragma unroll
+        for (int j = 0; j < NOB; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[j][r] += mb[w * WSTRIDE + (j * 4 + r) * 64 + lane] * cw;
+    }
+
+    // Partial for (bh, qt, split): O rows (unnormalised), m and l per query.
+    const size_t pidx = ((size_t)bh * p.nqt + qt) * p.num_splits + split;
+    float* po = p.part_o + pidx * 16 * D;
+    float* pml = p.part_ml + pidx * 32;
+    if (lg == 0) {
+        pml[lr] = mn;
+        pml[16 + lr] = l;
+    }
+    // lane holds O^T[dv][q = lr] for dv = 64hh + VW*(4lg + r) + j
+#pragma unroll
+    for (int hh = 0; hh < NVL; ++hh)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int dv0 = 64 * hh + VW * (4 * lg + r);
+            if constexpr (VW == 4) {
+                f32x4 t = {o[hh * 4 + 0][r], o[hh * 4 + 1][r], o[hh * 4 + 2][r], o[hh * 4 + 3][r]};
+                *reinterpret_cast<f32x4*>(po + lr * D + dv0) = t;
+            } else {
+#pragma unroll
+                for (int j = 0; j < VW; ++j) po[lr * D + dv0 + j] = o[hh * VW + j][r];
+            }
+        }
+}
+
+// Combine split partials: O = sum_s 2^((m_s - M) c) O_s / sum_s 2^((m_s - M) c) l_s.
+// One thread per (bh, query, 4 consecutive dv).
+__device__ __forceinline__ void merge_body(const FaParams& p, int D) {
+    const int seq_q = p.seq_q, d = p.d;
+    const int nchunk = (d + 3) / 4;
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t total = (size_t)p.bh * seq_q * nchunk;
+    if (gid >= total) return;
+    const int chunk = (int)(gid % nchunk);
+    const size_t row = gid / nchunk;           // bh * seq_q + q
+    const int q = (int)(row % seq_q);
+    const int bh = (int)(row / seq_q);
+    const int qt = q / 16, qi = q % 16;
+    const float c = p.scale_log2e;
+    const size_t pbase = ((size_t)bh * p.nqt + qt) * p.num_splits;
+    float M = FA_NEG_INF;
+    for (int s = 0; s < p.num_splits; ++s) M = fmaxf(M, p.part_ml[(pbase + s) * 32 + qi]);
+    const float Mu = (M == FA_NEG_INF) ? 0.0f : M;
+    float L = 0.0f;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = 0; s < p.num_splits; ++s) {
+        const float* ml = p.part_ml + (pbase + s) * 32;
+        const float w = rescale_factor(ml[qi], Mu, c);
+        L += ml[16 + qi] * w;
+        const f32x4 v = *reinterpret_cast<const f32x4*>(p.part_o + ((pbase + s) * 16 + qi) * D + 4 * chunk);
+        acc += v * w;
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    float* orow = p.out + row * d;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        if (4 * chunk + e < d) orow[4 * chunk + e] = acc[e] * inv;
+}
+
+// ---------------------------------------------------------------------------
+// Named entry points for hipModuleGetFunction.
+// ---------------------------------------------------------------------------
+// fa_prefill_v{V}_d{D}_{L}: L = 0 scalar loads, 1 vector loads, 2 LDS DMA (v3).
+#define FA_PREFILL(D, VAR, LD)                                                                   \
+    extern "C" __global__ void __launch_bounds__(512, 1) fa_prefill_v##VAR##_d##D##_##LD(FaParams p) { \
+        prefill_body<D, VAR, LD>(p);                                                             \
+    }
+#define FA_PREFILL_ALL(D)  \
+    FA_PREFILL(D, 1, 0)    \
+    FA_PREFILL(D, 1, 1)    \
+    FA_PREFILL(D, 2, 0)    \
+    FA_PREFILL(D, 2, 1)    \
+    FA_PREFILL(D, 3, 0)    \
+    FA_PREFILL(D, 3, 1)    \
+    FA_PREFILL(D, 3, 2)
+
+FA_PREFILL_ALL(32)
+FA_PREFILL_ALL(64)
+FA_PREFILL_ALL(128)
+FA_PREFILL_ALL(256)
+
+#define FA_DECODE(D, VEC) \
+    extern "C" __global__ void __launch_bounds__(256, 2) fa_decode_d##D##_##VEC(FaParams p) { decode_body<D, VEC != 0>(p); }
+FA_DECODE(32, 1)
+FA_DECODE(32, 0)
+FA_DECODE(64, 1)
+FA_DECODE(64, 0)
+FA_DECODE(128, 1)
+FA_DECODE(128, 0)
+FA_DECODE(256, 1)
+FA_DECODE(256, 0)
+
+#define FA_MERGE(D) \
+    extern "C" __global__ void __launch_bounds__(256) fa_merge_d##D(FaParams p) { merge_body(p, D); }
+FA_MERGE(32)
+FA_MERGE(64)
+FA_MERGE(128)
+FA_MERGE(256)

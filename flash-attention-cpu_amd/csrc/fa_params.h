@@ -1,0 +1,29 @@
+// fa_params.h -- the one argument block every kernel in fa_kernels.hip takes.
+//
+// Passed by value through hipModuleLaunchKernel; the host library fills it.
+// Plain C layout (pointers, then 32-bit fields) so host and device agree.
+#ifndef FA_PARAMS_H
+#define FA_PARAMS_H
+
+#include <stdint.h>
+
+typedef struct FaParams {
+    const float* q;      // [bh, seq_q, d]
+    const float* k;      // [bh, seq_k, d]
+    const float* v;      // [bh, seq_k, d]
+    float* out;          // [bh, seq_q, d]
+    float* part_o;       // split-KV partial O: [bh, nqt, num_splits, 16, D]
+    float* part_ml;      // split-KV partial (m, l): [bh, nqt, num_splits, 2, 16]
+    int bh;              // batch * heads
+    int seq_q;
+    int seq_k;
+    int d;               // true d_head (kernels pad to D)
+    int causal;          // top-left aligned: key j visible to query i iff j <= i
+    float scale_log2e;   // (1/sqrt(d) computed in f32) * log2(e)
+    int nqb;             // prefill: query blocks of 128 rows
+    int nqt;             // split-KV: query tiles of 16 rows
+    int num_splits;      // split-KV: key splits per (bh, query tile)
+    int split_len;       // split-KV: keys per split (multiple of 64)
+} FaParams;
+
+#endif

@@ -1,0 +1,251 @@
+"""Python view of libfa_hip.so (the C ABI in include/fa_hip.h).
+
+Mirrors the public API of the reference crate amaye15/flash-attention-cpu
+(src/lib.rs:78-87) with the same names, argument order and meaning:
+
+    flash_attention_v1/v2/v3(q, k, v, seq_len_q, seq_len_k, d_head, config, out)
+    flash_attention_multihead_v1/v2/v3(q, k, v, batch, heads, seq_len_q,
+                                       seq_len_k, d_head, config, out)
+    flash_attention = flash_attention_v2
+    flash_attention_multihead = flash_attention_multihead_v2
+    FlashAttentionConfig(block_size_q=64, block_size_kv=128, causal=False)
+
+``q``/``k``/``v`` are float32 buffers (numpy arrays) and ``out`` is written
+in place, as ``&mut [f32]`` is in the crate.  Where the crate panics on a
+shape mismatch (src/common.rs:51-54) these raise ``ShapeMismatch`` with the
+same message.  All compute runs on the GPU; without a usable HIP device the
+calls raise ``FaError`` -- there is no CPU fallback.
+
+``attention_device`` is the device-resident form (raw device pointers and a
+HIP stream, e.g. from torch tensors), used by the benchmark.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG_DIR, "libfa_hip.so")
+MODULE_PATH = os.path.join(_PKG_DIR, "fa_kernels.hsaco")
+
+FA_OK = 0
+FA_ERR_Q_SHAPE = 1
+FA_ERR_K_SHAPE = 2
+FA_ERR_V_SHAPE = 3
+FA_ERR_OUT_SHAPE = 4
+FA_ERR_INVALID_ARG = 5
+FA_ERR_UNSUPPORTED = 6
+FA_ERR_NO_DEVICE = 7
+FA_ERR_MODULE = 8
+FA_ERR_ALLOC = 9
+FA_ERR_LAUNCH = 10
+FA_ERR_COPY = 11
+
+PATH_AUTO = 0
+PATH_PREFILL = 1
+PATH_SPLITKV = 2
+
+# Every symbol include/fa_hip.h declares.
+EXPORTED_SYMBOLS = (
+    "fa_status_string", "fa_config_default",
+    "fa_v1", "fa_v2", "fa_v3", "fa_attention",
+    "fa_multihead_v1", "fa_multihead_v2", "fa_multihead_v3", "fa_attention_multihead",
+    "fa_device_v1", "fa_device_v2", "fa_device_v3", "fa_device_ex",
+    "fa_init", "fa_describe_launch",
+)
+
+
+class FaError(RuntimeError):
+    """A non-zero status from libfa_hip.so."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+
+
+class ShapeMismatch(FaError, AssertionError):
+    """The crate's shape assert (src/common.rs:51-54) failed."""
+
+
+@dataclass
+class FlashAttentionConfig:
+    """FlashAttentionConfig (src/common.rs:16-36)."""
+
+    block_size_q: int = 64
+    block_size_kv: int = 128
+    causal: bool = False
+
+
+class _CConfig(ctypes.Structure):
+    _fields_ = [("block_size_q", ctypes.c_size_t), ("block_size_kv", ctypes.c_size_t),
+                ("causal", ctypes.c_uint8)]
+
+
+class _COpts(ctypes.Structure):
+    _fields_ = [("softmax_scale", ctypes.c_float), ("path", ctypes.c_int), ("num_splits", ctypes.c_int)]
+
+
+_lib = None
+_F = ctypes.POINTER(ctypes.c_float)
+_SZ = ctypes.c_size_t
+_CFG = ctypes.POINTER(_CConfig)
+_OPTS = ctypes.POINTER(_COpts)
+
+
+def lib() -> ctypes.CDLL:
+    """Load libfa_hip.so (built by flash-attention-cpu_amd/build.py)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise FaError(FA_ERR_MODULE, f"{LIB_PATH} is not built; run flash-attention-cpu_amd/build.py")
+    L = ctypes.CDLL(LIB_PATH)
+    L.fa_status_string.restype = ctypes.c_char_p
+    L.fa_status_string.argtypes = [ctypes.c_int]
+    L.fa_config_default.restype = _CConfig
+    single = [_F, _SZ, _F, _SZ, _F, _SZ, _SZ, _SZ, _SZ, _CFG, _F, _SZ]
+    for name in ("fa_v1", "fa_v2", "fa_v3", "fa_attention"):
+        getattr(L, name).argtypes = single
+        getattr(L, name).restype = ctypes.c_int
+    multi = [_F, _SZ, _F, _SZ, _F, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _CFG, _F, _SZ]
+    for name in ("fa_multihead_v1", "fa_multihead_v2", "fa_multihead_v3", "fa_attention_multihead"):
+        getattr(L, name).argtypes = multi
+        getattr(L, name).restype = ctypes.c_int
+    dev = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, _SZ, _SZ, _SZ, _SZ, _SZ,
+           _CFG, ctypes.c_void_p]
+    for name in ("fa_device_v1", "fa_device_v2", "fa_device_v3"):
+        getattr(L, name).argtypes = dev
+        getattr(L, name).restype = ctypes.c_int
+    L.fa_device_ex.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                               ctypes.c_void_p, _SZ, _SZ, _SZ, _SZ, _SZ, _CFG, _OPTS, ctypes.c_void_p]
+    L.fa_device_ex.restype = ctypes.c_int
+    L.fa_init.restype = ctypes.c_int
+    L.fa_describe_launch.argtypes = [ctypes.c_int, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_int, _OPTS,
+                                     ctypes.c_char_p, _SZ]
+    L.fa_describe_launch.restype = ctypes.c_int
+    _lib = L
+    return L
+
+
+def status_string(status: int) -> str:
+    return lib().fa_status_string(int(status)).decode()
+
+
+def _check(status: int) -> None:
+    if status == FA_OK:
+        return
+    msg = status_string(status)
+    if status in (FA_ERR_Q_SHAPE, FA_ERR_K_SHAPE, FA_ERR_V_SHAPE, FA_ERR_OUT_SHAPE):
+        raise ShapeMismatch(status, msg)
+    raise FaError(status, msg)
+
+
+def _cfg(config: FlashAttentionConfig | None) -> _CConfig:
+    if config is None:
+        return lib().fa_config_default()
+    return _CConfig(int(config.block_size_q), int(config.block_size_kv), 1 if config.causal else 0)
+
+
+def _in(a) -> tuple[np.ndarray, int]:
+    arr = np.ascontiguousarray(a, dtype=np.float32)
+    return arr, arr.size
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(_F) if a.size else None
+
+
+def _out(out) -> np.ndarray:
+    if not isinstance(out, np.ndarray) or out.dtype != np.float32 or not out.flags.c_contiguous:
+        raise TypeError("out must be a C-contiguous numpy float32 array (written in place)")
+    return out
+
+
+def _single(name, q, k, v, seq_len_q, seq_len_k, d_head, config, out):
+    q, nq = _in(q)
+    k, nk = _in(k)
+    v, nv = _in(v)
+    out = _out(out)
+    cfg = _cfg(config)
+    _check(getattr(lib(), name)(_ptr(q), nq, _ptr(k), nk, _ptr(v), nv, seq_len_q, seq_len_k, d_head,
+                                ctypes.byref(cfg), _ptr(out), out.size))
+
+
+def _multi(name, q, k, v, batch, heads, seq_len_q, seq_len_k, d_head, config, out):
+    q, nq = _in(q)
+    k, nk = _in(k)
+    v, nv = _in(v)
+    out = _out(out)
+    cfg = _cfg(config)
+    _check(getattr(lib(), name)(_ptr(q), nq, _ptr(k), nk, _ptr(v), nv, batch, heads, seq_len_q, seq_len_k,
+                                d_head, ctypes.byref(cfg), _ptr(out), out.size))
+
+
+def flash_attention_v1(q, k, v, seq_len_q, seq_len_k, d_head, config, out) -> None:
+    """flash_attention_v1 (src/v1.rs:51)."""
+    _single("fa_v1", q, k, v, seq_len_q, seq_len_k, d_head, config, out)
+
+
+def flash_attention_v2(q, k, v, seq_len_q, seq_len_k, d_head, config, out) -> None:
+    """flash_attention_v2 (src/v2.rs:49)."""
+    _single("fa_v2", q, k, v, seq_len_q, seq_len_k, d_head, config, out)
+
+
+def flash_attention_v3(q, k, v, seq_len_q, seq_len_k, d_head, config, out) -> None:
+    """flash_attention_v3 (src/v3.rs:61)."""
+    _single("fa_v3", q, k, v, seq_len_q, seq_len_k, d_head, config, out)
+
+
+def flash_attention_multihead_v1(q, k, v, batch, heads, seq_len_q, seq_len_k, d_head, config, out) -> None:
+    """flash_attention_multihead_v1 (src/v1.rs:134)."""
+    _multi("fa_multihead_v1", q, k, v, batch, heads, seq_len_q, seq_len_k, d_head, config, out)
+
+
+def flash_attention_multihead_v2(q, k, v, batch, heads, seq_len_q, seq_len_k, d_head, config, out) -> None:
+    """flash_attention_multihead_v2 (src/v2.rs:132)."""
+    _multi("fa_multihead_v2", q, k, v, batch, heads, seq_len_q, seq_len_k, d_head, config, out)
+
+
+def flash_attention_multihead_v3(q, k, v, batch, heads, seq_len_q, seq_len_k, d_head, config, out) -> None:
+    """flash_attention_multihead_v3 (src/v3.rs:144)."""
+    _multi("fa_multihead_v3", q, k, v, batch, heads, seq_len_q, seq_len_k, d_head, config, out)
+
+
+# Backward-compatible aliases (src/lib.rs:86-87).
+flash_attention = flash_attention_v2
+flash_attention_multihead = flash_attention_multihead_v2
+
+VARIANTS = {1: flash_attention_v1, 2: flash_attention_v2, 3: flash_attention_v3}
+MULTIHEAD_VARIANTS = {1: flash_attention_multihead_v1, 2: flash_attention_multihead_v2,
+                      3: flash_attention_multihead_v3}
+
+
+def attention_device(variant: int, q_ptr: int, k_ptr: int, v_ptr: int, batch: int, heads: int,
+                     seq_len_q: int, seq_len_k: int, d_head: int, causal: bool, out_ptr: int,
+                     stream: int = 0, softmax_scale: float | None = None, path: int = PATH_AUTO,
+                     num_splits: int = 0) -> None:
+    """Queue one call on device pointers (fa_device_ex); returns when queued."""
+    cfg = _CConfig(64, 128, 1 if causal else 0)
+    opts = _COpts(float(softmax_scale) if softmax_scale else 0.0, int(path), int(num_splits))
+    _check(lib().fa_device_ex(int(variant), ctypes.c_void_p(stream), ctypes.c_void_p(q_ptr),
+                              ctypes.c_void_p(k_ptr), ctypes.c_void_p(v_ptr), batch, heads, seq_len_q,
+                              seq_len_k, d_head, ctypes.byref(cfg), ctypes.byref(opts),
+                              ctypes.c_void_p(out_ptr)))
+
+
+def describe_launch(variant: int, batch: int, heads: int, seq_len_q: int, seq_len_k: int, d_head: int,
+                    causal: bool, path: int = PATH_AUTO, num_splits: int = 0) -> str:
+    """Kernel name(s) and grid a call would launch (launches nothing)."""
+    opts = _COpts(0.0, int(path), int(num_splits))
+    buf = ctypes.create_string_buffer(512)
+    _check(lib().fa_describe_launch(int(variant), batch, heads, seq_len_q, seq_len_k, d_head,
+                                    1 if causal else 0, ctypes.byref(opts), buf, len(buf)))
+    return buf.value.decode()
+
+
+def init() -> None:
+    """Load the gfx950 code object on the current device; raises without one."""
+    _check(lib().fa_init())

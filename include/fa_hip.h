@@ -1,0 +1,166 @@
+/*
+ * fa_hip.h -- C ABI of the MI355X FlashAttention library (libfa_hip.so).
+ *
+ * The drop-in boundary for the reference crate amaye15/flash-attention-cpu:
+ * every entry point below replaces one public Rust function of that crate
+ * (cited per declaration) with the same argument meaning: row-major f32
+ * Q/K/V/O, [batch, heads, seq, d_head] for the multi-head forms, the causal
+ * flag of FlashAttentionConfig, and the implicit softmax scale
+ * 1/sqrt(d_head) computed in f32.  Rust slices become (pointer, length)
+ * pairs so the crate's shape asserts keep their meaning; a failed assert
+ * becomes a non-zero status instead of a panic, naming the same operand.
+ *
+ * All compute runs on the GPU (hand-written gfx950 kernels loaded from a
+ * code object with hipModuleLoad); there is no CPU fallback.  Host-slice
+ * entry points copy to device memory, launch, copy back and synchronise;
+ * the _device forms take caller-owned device pointers and the caller's HIP
+ * stream and return as soon as the kernels are queued.
+ *
+ * Thread safety: every entry point may be called from several threads at
+ * once (the crate's functions are Sync).  Host-slice calls on one device
+ * are serialised internally.
+ */
+#ifndef FA_HIP_H
+#define FA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define FA_OK 0
+#define FA_ERR_Q_SHAPE 1      /* "q shape mismatch"   src/common.rs:51, :87 */
+#define FA_ERR_K_SHAPE 2      /* "k shape mismatch"   src/common.rs:52, :88 */
+#define FA_ERR_V_SHAPE 3      /* "v shape mismatch"   src/common.rs:53, :89 */
+#define FA_ERR_OUT_SHAPE 4    /* "out shape mismatch" src/common.rs:54, :90 */
+#define FA_ERR_INVALID_ARG 5  /* NULL pointer with a non-zero length, bad variant/option */
+#define FA_ERR_UNSUPPORTED 6  /* d_head > 256, or a size beyond 32-bit row indexing */
+#define FA_ERR_NO_DEVICE 7    /* no HIP device visible */
+#define FA_ERR_MODULE 8       /* code object missing / unloadable (FA_HIP_MODULE) */
+#define FA_ERR_ALLOC 9        /* device allocation failed */
+#define FA_ERR_LAUNCH 10      /* kernel launch failed */
+#define FA_ERR_COPY 11        /* host<->device copy or synchronisation failed */
+
+/* Human-readable text for a status code (static storage). */
+const char* fa_status_string(int status);
+
+/* ---- configuration ------------------------------------------------------
+ * Mirrors FlashAttentionConfig (src/common.rs:16-36).  block_size_q and
+ * block_size_kv are accepted for signature parity; the GPU tiles are fixed
+ * per d_head and results do not depend on block sizes beyond rounding, as
+ * in the reference (tests/correctness.rs:137-171).  causal: key j is
+ * visible to query i iff j <= i, in absolute indices (src/naive.rs:37). */
+typedef struct fa_config {
+    size_t block_size_q;   /* default 64  */
+    size_t block_size_kv;  /* default 128 */
+    uint8_t causal;        /* default 0   */
+} fa_config;
+
+/* FlashAttentionConfig::default() -- src/common.rs:28-36 */
+fa_config fa_config_default(void);
+
+/* ---- single head, host slices ------------------------------------------
+ * q: [seq_len_q, d_head], k/v: [seq_len_k, d_head], out: [seq_len_q, d_head].
+ * Checks q/k/v/out lengths in that order (check_shapes, src/common.rs:41-57);
+ * if seq_len_q, seq_len_k or d_head is 0 returns FA_OK without touching out.
+ * config == NULL means fa_config_default(). */
+
+/* flash_attention_v1 -- src/v1.rs:51-123 (FA-1: per-step normalisation,
+ * no causal tile skip) */
+int fa_v1(const float* q, size_t q_len, const float* k, size_t k_len, const float* v, size_t v_len,
+          size_t seq_len_q, size_t seq_len_k, size_t d_head, const fa_config* config, float* out,
+          size_t out_len);
+/* flash_attention_v2 -- src/v2.rs:49-121 (FA-2: deferred normalisation,
+ * causal skip of fully-future tiles) */
+int fa_v2(const float* q, size_t q_len, const float* k, size_t k_len, const float* v, size_t v_len,
+          size_t seq_len_q, size_t seq_len_k, size_t d_head, const fa_config* config, float* out,
+          size_t out_len);
+/* flash_attention_v3 -- src/v3.rs:61-133 (v2 with the next tile's QK^T
+ * overlapped with the current softmax + PV) */
+int fa_v3(const float* q, size_t q_len, const float* k, size_t k_len, const float* v, size_t v_len,
+          size_t seq_len_q, size_t seq_len_k, size_t d_head, const fa_config* config, float* out,
+          size_t out_len);
+/* flash_attention (alias of v2) -- src/lib.rs:87 */
+int fa_attention(const float* q, size_t q_len, const float* k, size_t k_len, const float* v,
+                 size_t v_len, size_t seq_len_q, size_t seq_len_k, size_t d_head,
+                 const fa_config* config, float* out, size_t out_len);
+
+/* ---- batched multi-head, host slices ----------------------------------
+ * q/out: [batch, heads, seq_len_q, d_head], k/v: [batch, heads, seq_len_k,
+ * d_head], contiguous (multihead_dispatch, src/common.rs:72-101).  All
+ * batch*heads slices run in one launch. */
+
+/* flash_attention_multihead_v1 -- src/v1.rs:134-159 */
+int fa_multihead_v1(const float* q, size_t q_len, const float* k, size_t k_len, const float* v,
+                    size_t v_len, size_t batch, size_t heads, size_t seq_len_q, size_t seq_len_k,
+                    size_t d_head, const fa_config* config, float* out, size_t out_len);
+/* flash_attention_multihead_v2 -- src/v2.rs:132-157 */
+int fa_multihead_v2(const float* q, size_t q_len, const float* k, size_t k_len, const float* v,
+                    size_t v_len, size_t batch, size_t heads, size_t seq_len_q, size_t seq_len_k,
+                    size_t d_head, const fa_config* config, float* out, size_t out_len);
+/* flash_attention_multihead_v3 -- src/v3.rs:144-169 */
+int fa_multihead_v3(const float* q, size_t q_len, const float* k, size_t k_len, const float* v,
+                    size_t v_len, size_t batch, size_t heads, size_t seq_len_q, size_t seq_len_k,
+                    size_t d_head, const fa_config* config, float* out, size_t out_len);
+/* flash_attention_multihead (alias of multihead v2) -- src/lib.rs:86 */
+int fa_attention_multihead(const float* q, size_t q_len, const float* k, size_t k_len,
+                           const float* v, size_t v_len, size_t batch, size_t heads,
+                           size_t seq_len_q, size_t seq_len_k, size_t d_head,
+                           const fa_config* config, float* out, size_t out_len);
+
+/* ---- device-resident, stream-ordered -----------------------------------
+ * Same computation as fa_multihead_vN on device pointers (hipMalloc'd or any
+ * device-accessible memory), queued on `stream` (a hipStream_t; NULL = the
+ * default stream).  No length checks are possible on raw pointers; zero
+ * dims return FA_OK with nothing queued.  v2/v3 pick the split-KV
+ * (flash-decoding) kernels for short query blocks against long key ranges;
+ * its workspace is allocated stream-ordered and released after the merge.
+ * These have no single counterpart in the reference (its API takes host
+ * slices); they are the device form of the multihead entry points. */
+int fa_device_v1(void* stream, const float* q, const float* k, const float* v, size_t batch,
+                 size_t heads, size_t seq_len_q, size_t seq_len_k, size_t d_head,
+                 const fa_config* config, float* out);
+int fa_device_v2(void* stream, const float* q, const float* k, const float* v, size_t batch,
+                 size_t heads, size_t seq_len_q, size_t seq_len_k, size_t d_head,
+                 const fa_config* config, float* out);
+int fa_device_v3(void* stream, const float* q, const float* k, const float* v, size_t batch,
+                 size_t heads, size_t seq_len_q, size_t seq_len_k, size_t d_head,
+                 const fa_config* config, float* out);
+
+/* ---- extension: explicit scale and path control ------------------------
+ * Not in the reference.  softmax_scale <= 0 or NaN keeps the reference's
+ * 1/sqrt(d_head).  path: FA_PATH_AUTO (what fa_device_vN does),
+ * FA_PATH_PREFILL (never split keys), FA_PATH_SPLITKV (always split; v2/v3
+ * only).  num_splits = 0 lets the library choose. */
+#define FA_PATH_AUTO 0
+#define FA_PATH_PREFILL 1
+#define FA_PATH_SPLITKV 2
+typedef struct fa_launch_opts {
+    float softmax_scale;
+    int path;
+    int num_splits;
+} fa_launch_opts;
+
+int fa_device_ex(int variant, void* stream, const float* q, const float* k, const float* v,
+                 size_t batch, size_t heads, size_t seq_len_q, size_t seq_len_k, size_t d_head,
+                 const fa_config* config, const fa_launch_opts* opts, float* out);
+
+/* ---- introspection -------------------------------------------------------
+ * fa_init loads the code object on the current device (done lazily by every
+ * entry point).  fa_describe_launch writes the kernel name(s) and grid the
+ * given call would launch, e.g. "fa_prefill_v2_d128_1 grid=512x1x1 block=512",
+ * launching nothing and needing no device (it plans for the current
+ * device's CU count, or 256 CUs when no device is visible); it returns the
+ * argument / support status the launch would return. */
+int fa_init(void);
+int fa_describe_launch(int variant, size_t batch, size_t heads, size_t seq_len_q, size_t seq_len_k,
+                       size_t d_head, int causal, const fa_launch_opts* opts, char* buf,
+                       size_t buf_len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FA_HIP_H */
