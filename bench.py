@@ -1,0 +1,267 @@
+#!/usr/bin/env python3
+"""Benchmark: FlashAttention forward on one MI355X.
+
+Headline (BASELINE.json metric, configs[1]): 32 heads x 2048 x 2048, d_head
+128, causal, f32, inputs resident in HBM.  A "step" is one attention call
+over that batch.  ``value`` is whole-job TFLOP/s (algorithmic FLOP
+4*d*visible_pairs*heads over wall time between synchronisations); the
+``roofline`` object prices the prefill kernel's own duration (HIP events on
+the launch stream) against the FP32-MFMA peak.  Decode shapes
+are reported in ``extra`` as GB/s against the 8 TB/s HBM peak.
+
+``cpu_baseline`` times the CPU oracle's v2 (oracle/, a C restatement of the
+reference crate's rayon + AVX-512/AVX2 path, src/v2.rs:160-385) on the same
+inputs, on the host cores, as a reported baseline only.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--variant 3]
+                       [--all] [--no-cpu-baseline]
+Prints exactly one JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "flash-attention-cpu_amd"))
+
+METRIC = "attention TFLOP/s f32 (32h×2048×d128 causal) + % FP32-MFMA peak; decode GB/s"
+PEAK_TFLOPS = 157.3     # MI355X dense FP32 MFMA
+PEAK_GBS = 8000.0       # MI355X HBM3E
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def visible_pairs(sq: int, sk: int, causal: bool) -> int:
+    if not causal:
+        return sq * sk
+    # key j visible to query i iff j <= i (top-left aligned)
+    n = min(sq, sk)
+    return n * (n + 1) // 2 + max(0, sq - sk) * sk
+
+
+def flops_of(bh, sq, sk, d, causal) -> int:
+    return 4 * d * visible_pairs(sq, sk, causal) * bh
+
+
+def bytes_of(bh, sq, sk, d) -> int:
+    return 4 * bh * d * (2 * sq + 2 * sk)
+
+
+class Workload:
+    def __init__(self, torch, name, bh, sq, sk, d, causal, qk_sigma=1.0, v_uniform=False):
+        self.name, self.bh, self.sq, self.sk, self.d, self.causal = name, bh, sq, sk, d, causal
+        dev = torch.device("cuda", 0)
+        gens = []
+        for seed in (1, 2, 3):   # seeds Q=1, K=2, V=3
+            g = torch.Generator(device=dev)
+            g.manual_seed(seed)
+            gens.append(g)
+        self.q = torch.randn(bh * sq * d, device=dev, generator=gens[0]) * qk_sigma
+        self.k = torch.randn(bh * sk * d, device=dev, generator=gens[1]) * qk_sigma
+        if v_uniform:
+            self.v = torch.rand(bh * sk * d, device=dev, generator=gens[2]) * 2.0 - 1.0
+        else:
+            self.v = torch.randn(bh * sk * d, device=dev, generator=gens[2])
+        self.o = torch.empty(bh * sq * d, device=dev)
+        self.flops = flops_of(bh, sq, sk, d, causal)
+        self.bytes = bytes_of(bh, sq, sk, d)
+
+
+def time_steps(torch, fa, wl: Workload, variant: int, steps: int, warmup: int):
+    """W warm-up calls, then K timed calls between synchronisations.
+
+    Returns (wall ms per step, kernel-stream ms per step from HIP events)."""
+    stream = torch.cuda.current_stream()
+    handle = stream.cuda_stream
+
+    def call():
+        fa.attention_device(variant, wl.q.data_ptr(), wl.k.data_ptr(), wl.v.data_ptr(), 1, wl.bh, wl.sq,
+                            wl.sk, wl.d, wl.causal, wl.o.data_ptr(), handle)
+
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        call()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    return (t1 - t0) * 1e3 / steps, e0.elapsed_time(e1) / steps
+
+
+def read_traffic(kernel: str, workload: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            table = json.load(f)
+    except (OSError, ValueError):
+        return None
+    ent = table.get(kernel)
+    if not ent or ent.get("workload") != workload:
+        return None
+    return ent.get("hbm_bytes_per_launch")
+
+
+def cpu_baseline(wl: Workload, budget_s: float):
+    """Oracle v2 (C restatement of the crate's CPU v2) on the same inputs."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle   # test infrastructure: the timed CPU baseline only
+
+    q = wl.q.cpu().numpy()
+    k = wl.k.cpu().numpy()
+    v = wl.v.cpu().numpy()
+    threads = min(16, os.cpu_count() or 1)
+    tier = oracle.best_tier()
+    oracle.run(2, q, k, v, wl.bh, wl.sq, wl.sk, wl.d, wl.causal, 64, 128, nthreads=threads)   # warm-up
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oracle.run(2, q, k, v, wl.bh, wl.sq, wl.sk, wl.d, wl.causal, 64, 128, nthreads=threads)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 200:
+            break
+    per_call = el / n
+    return {
+        "value": round(wl.flops / per_call / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{wl.name}: full workload ({wl.bh} heads), {n} calls after 1 warm-up, "
+                   f"{per_call * 1e3:.1f} ms/call, oracle v2 {oracle.TIER_NAMES[tier]} tier, "
+                   f"Br=64 Bc=128, {threads} threads"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--variant", type=int, default=3, choices=(1, 2, 3))
+    ap.add_argument("--all", action="store_true", help="also time configs 1, 3, 5, 5c")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="only run 5 plain device copies of N MiB (rocprofv3 PMC scale reference) and exit")
+    ap.add_argument("--only-config2", action="store_true", help="time only the headline workload")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X; "
+              "heads shard across GPUs with no communication (see DESIGN.md), run with --gpus 1",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    if args.calibrate_copy_mib:
+        n = args.calibrate_copy_mib * (1 << 20) // 4
+        x = torch.ones(n, device="cuda")
+        y = torch.empty_like(x)
+        for _ in range(5):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        log(f"[bench] copied {args.calibrate_copy_mib} MiB x5")
+        return 0
+
+    import flash_attention_amd as fa
+
+    fa.init()
+    extra = {}
+
+    head = Workload(torch, "config2: 32h x 2048 x 2048, d128, causal, N(0,1)", 32, 2048, 2048, 128, True)
+    kernel = fa.describe_launch(args.variant, 1, head.bh, head.sq, head.sk, head.d, head.causal).split()[0]
+    ms_step, ms_kernel = time_steps(torch, fa, head, args.variant, args.steps, args.warmup)
+    value = head.flops / (ms_step * 1e-3) / 1e12
+    achieved = head.flops / (ms_kernel * 1e-3) / 1e12
+    log(f"[bench] config2 v{args.variant}: {ms_step * 1e3:.1f} us/step wall, {ms_kernel * 1e3:.1f} us kernel, "
+        f"{value:.2f} TFLOP/s")
+
+    for var in (() if args.only_config2 else (1, 2, 3)):
+        if var == args.variant:
+            m_w, m_k = ms_step, ms_kernel
+        else:
+            m_w, m_k = time_steps(torch, fa, head, var, max(5, args.steps // 2), args.warmup)
+        extra[f"config2_v{var}"] = {"us_per_call": round(m_k * 1e3, 1),
+                                    "tflops": round(head.flops / (m_k * 1e-3) / 1e12, 2),
+                                    "pct_fp32_mfma_peak": round(100 * head.flops / (m_k * 1e-3) / 1e12
+                                                                / PEAK_TFLOPS, 1)}
+        log(f"[bench] config2 v{var}: {m_k * 1e3:.1f} us, {extra[f'config2_v{var}']['tflops']} TFLOP/s")
+
+    # Decode shapes: split-KV + merge, bandwidth-bound.
+    k_dec = v_dec = None
+    for sq in (() if args.only_config2 else (1, 16)):
+        wl = Workload(torch, f"config4 seq_q={sq}", 32, sq, 32768, 128, False)
+        if k_dec is not None:   # share K/V (1 GiB) between the two decode shapes
+            wl.k, wl.v = k_dec, v_dec
+        k_dec, v_dec = wl.k, wl.v
+        _, m_k = time_steps(torch, fa, wl, 2, max(10, args.steps), args.warmup)
+        gbs = wl.bytes / (m_k * 1e-3) / 1e9
+        extra[f"config4_decode_sq{sq}"] = {"us_per_call": round(m_k * 1e3, 1), "gbs": round(gbs, 1),
+                                           "pct_hbm_peak": round(100 * gbs / PEAK_GBS, 1),
+                                           "kernels": fa.describe_launch(2, 1, 32, sq, 32768, 128, False)}
+        log(f"[bench] config4 seq_q={sq}: {m_k * 1e3:.1f} us, {gbs:.0f} GB/s")
+        del wl
+    del k_dec, v_dec
+    torch.cuda.empty_cache()
+
+    if args.all:
+        for name, shape in (("config1", (1, 256, 256, 64, False, 1.0, False)),
+                            ("config3", (8, 16384, 16384, 128, True, 1.0, False)),
+                            ("config5", (16, 4096, 1024, 256, False, 3.0, True)),
+                            ("config5c", (16, 1000, 1000, 256, True, 3.0, True))):
+            bh, sq, sk, d, causal, sig, vu = shape
+            wl = Workload(torch, name, bh, sq, sk, d, causal, sig, vu)
+            for var in (1, 2, 3):
+                steps = 3 if name == "config3" else max(5, args.steps // 2)
+                _, m_k = time_steps(torch, fa, wl, var, steps, 2)
+                tf = wl.flops / (m_k * 1e-3) / 1e12
+                extra[f"{name}_v{var}"] = {"us_per_call": round(m_k * 1e3, 1), "tflops": round(tf, 2),
+                                           "pct_fp32_mfma_peak": round(100 * tf / PEAK_TFLOPS, 1)}
+                log(f"[bench] {name} v{var}: {m_k * 1e3:.1f} us, {tf:.2f} TFLOP/s")
+            del wl
+            torch.cuda.empty_cache()
+
+    traffic = read_traffic(kernel, "config2")
+    result = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "config2: multihead prefill, 32 heads x 2048 x 2048, d_head 128, causal, "
+                               "f32 N(0,1) Q/K/V (seeds 1/2/3), [heads, seq, d] contiguous",
+                   "heads": 32, "seq_q": 2048, "seq_k": 2048, "d_head": 128, "causal": True,
+                   "variant": f"v{args.variant}", "kernel": kernel},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": traffic},
+        "extra": extra,
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(head, args.cpu_seconds)
+        log(f"[bench] cpu baseline: {result['cpu_baseline']}")
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -95,11 +95,28 @@ _CFG = ctypes.POINTER(_CConfig)
 _OPTS = ctypes.POINTER(_COpts)
 
 
+def _share_hip_runtime_with_torch() -> None:
+    """Load torch (if installed) before libfa_hip.so.
+
+    PyTorch-ROCm wheels bundle their own libamdhip64 and resolve it by path;
+    if libfa_hip.so pulled in /opt/rocm's copy first, a later ``import torch``
+    would load a second HIP runtime and find no GPU.  Loaded the other way
+    round, libfa_hip.so binds to torch's already-loaded libamdhip64.so.7 and
+    the process has one runtime.  Set FA_NO_TORCH_PRELOAD=1 to skip."""
+    if os.environ.get("FA_NO_TORCH_PRELOAD"):
+        return
+    try:
+        import torch  # noqa: F401
+    except Exception:   # torch absent or broken: nothing to share with
+        pass
+
+
 def lib() -> ctypes.CDLL:
     """Load libfa_hip.so (built by flash-attention-cpu_amd/build.py)."""
     global _lib
     if _lib is not None:
         return _lib
+    _share_hip_runtime_with_torch()
     if not os.path.exists(LIB_PATH):
         raise FaError(FA_ERR_MODULE, f"{LIB_PATH} is not built; run flash-attention-cpu_amd/build.py")
     L = ctypes.CDLL(LIB_PATH)

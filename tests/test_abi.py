@@ -1,0 +1,209 @@
+"""Host-side checks of the C ABI (libfa_hip.so) that need no GPU.
+
+* the library loads and exports every function include/fa_hip.h declares;
+* the crate's shape asserts (src/common.rs:51-54, :87-90) map to status
+  codes in the same order (q, k, v, out), checked before any device access;
+* zero-sized dims return FA_OK and leave out untouched (src/common.rs:56,
+  tests/correctness.rs:465-504);
+* without a visible device every compute entry point fails loudly with
+  FA_ERR_NO_DEVICE (no CPU fallback exists);
+* launch planning (fa_describe_launch): kernel choice per d_head, load path,
+  split-KV for short queries, v1 never split, unsupported d_head.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+import flash_attention_amd as fa
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fa_hip.h")
+
+
+def _has_gpu() -> bool:
+    return os.path.exists("/dev/kfd")
+
+
+def declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fa_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    names = declared_functions()
+    assert len(names) >= 16
+    lib = fa.lib()
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in fa_hip.h but not exported"
+    assert sorted(fa.EXPORTED_SYMBOLS) == names
+    out = subprocess.run(["nm", "-D", "--defined-only", fa.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r" T (fa_[a-z0-9_]+)$", out, flags=re.M))
+    assert exported == set(names)
+
+
+def test_product_library_does_not_link_the_oracle():
+    out = subprocess.run(["ldd", fa.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    assert "oracle" not in out
+    dyn = subprocess.run(["nm", "-D", fa.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    assert "oracle_" not in dyn
+
+
+def test_status_strings():
+    assert fa.status_string(fa.FA_OK) == "ok"
+    assert fa.status_string(fa.FA_ERR_Q_SHAPE) == "q shape mismatch"
+    assert fa.status_string(fa.FA_ERR_K_SHAPE) == "k shape mismatch"
+    assert fa.status_string(fa.FA_ERR_V_SHAPE) == "v shape mismatch"
+    assert fa.status_string(fa.FA_ERR_OUT_SHAPE) == "out shape mismatch"
+    for code in range(5, 12):
+        assert fa.status_string(code) not in ("ok", "unknown status")
+    assert fa.status_string(999) == "unknown status"
+
+
+def test_config_default_mirrors_reference():
+    c = fa.lib().fa_config_default()
+    assert (c.block_size_q, c.block_size_kv, c.causal) == (64, 128, 0)   # src/common.rs:28-36
+
+
+@pytest.mark.parametrize("variant", (1, 2, 3))
+def test_shape_mismatch_order_and_messages(variant):
+    f = fa.VARIANTS[variant]
+    sq, sk, d = 4, 4, 8
+    q = np.zeros(sq * d, np.float32)
+    k = np.zeros(sk * d, np.float32)
+    v = np.zeros(sk * d, np.float32)
+    cfg = fa.FlashAttentionConfig()
+    # every operand wrong: q is reported first, as check_shapes asserts q first
+    with pytest.raises(fa.ShapeMismatch, match="^q shape mismatch$"):
+        f(q[:-1], k[:-1], v[:-1], sq, sk, d, cfg, np.zeros(sq * d - 1, np.float32))
+    with pytest.raises(fa.ShapeMismatch, match="^k shape mismatch$"):
+        f(q, k[:-1], v[:-1], sq, sk, d, cfg, np.zeros(sq * d - 1, np.float32))
+    with pytest.raises(fa.ShapeMismatch, match="^v shape mismatch$"):
+        f(q, k, v[:-1], sq, sk, d, cfg, np.zeros(sq * d - 1, np.float32))
+    with pytest.raises(fa.ShapeMismatch, match="^out shape mismatch$"):
+        f(q, k, v, sq, sk, d, cfg, np.zeros(sq * d - 1, np.float32))
+    # the ShapeMismatch is also an AssertionError, as the crate's assert_eq! panics
+    with pytest.raises(AssertionError):
+        f(q[:-1], k, v, sq, sk, d, cfg, np.zeros(sq * d, np.float32))
+
+
+@pytest.mark.parametrize("variant", (1, 2, 3))
+def test_multihead_shape_mismatch(variant):
+    f = fa.MULTIHEAD_VARIANTS[variant]
+    b, h, sq, sk, d = 2, 2, 4, 4, 8
+    q = np.zeros(b * h * sq * d, np.float32)
+    k = np.zeros(b * h * sk * d, np.float32)
+    with pytest.raises(fa.ShapeMismatch, match="q shape"):
+        f(q[:-1], k, k, b, h, sq, sk, d, None, np.zeros(b * h * sq * d, np.float32))
+    with pytest.raises(fa.ShapeMismatch, match="out shape"):
+        f(q, k, k, b, h, sq, sk, d, None, np.zeros(b * h * sq * d + 1, np.float32))
+
+
+@pytest.mark.parametrize("variant", (1, 2, 3))
+def test_zero_sized_dims_leave_out_untouched_without_device(variant):
+    f = fa.VARIANTS[variant]
+    d = 8
+    out = np.full(4 * d, 12.5, np.float32)
+    f(np.ones(4 * d, np.float32), np.zeros(0, np.float32), np.zeros(0, np.float32), 4, 0, d, None, out)
+    assert np.all(out == 12.5)
+    f(np.zeros(0, np.float32), np.ones(4 * d, np.float32), np.ones(4 * d, np.float32), 0, 4, d, None,
+      np.zeros(0, np.float32))
+    f(np.zeros(0, np.float32), np.zeros(0, np.float32), np.zeros(0, np.float32), 4, 4, 0, None,
+      np.zeros(0, np.float32))
+    m = fa.MULTIHEAD_VARIANTS[variant]
+    out = np.full(0, 12.5, np.float32)
+    m(np.zeros(0, np.float32), np.zeros(0, np.float32), np.zeros(0, np.float32), 0, 3, 4, 4, d, None, out)
+
+
+@pytest.mark.skipif(_has_gpu(), reason="checks the no-device path")
+def test_no_device_fails_loudly():
+    with pytest.raises(fa.FaError) as e:
+        fa.init()
+    assert e.value.status == fa.FA_ERR_NO_DEVICE
+    d = 16
+    out = np.full(8 * d, 7.0, np.float32)
+    for variant in (1, 2, 3):
+        with pytest.raises(fa.FaError) as e:
+            fa.VARIANTS[variant](np.ones(8 * d, np.float32), np.ones(8 * d, np.float32),
+                                 np.ones(8 * d, np.float32), 8, 8, d, None, out)
+        assert e.value.status == fa.FA_ERR_NO_DEVICE
+        assert np.all(out == 7.0)
+    with pytest.raises(fa.FaError) as e:
+        fa.attention_device(2, 16, 16, 16, 1, 1, 8, 8, d, False, 16)
+    assert e.value.status == fa.FA_ERR_NO_DEVICE
+
+
+def test_bad_code_object_path_fails_with_module_or_no_device():
+    code = ("import sys; sys.path.insert(0, %r); import flash_attention_amd as fa\n"
+            "try:\n    fa.init(); print('ok')\nexcept fa.FaError as e:\n    print(e.status)\n"
+            % os.path.join(ROOT, "flash-attention-cpu_amd"))
+    env = dict(os.environ, FA_HIP_MODULE="/nonexistent/fa_kernels.hsaco")
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env,
+                         timeout=120).stdout.strip()
+    expect = fa.FA_ERR_MODULE if _has_gpu() else fa.FA_ERR_NO_DEVICE
+    assert out == str(expect)
+
+
+def describe(variant, b, h, sq, sk, d, causal, path=fa.PATH_AUTO, splits=0):
+    return fa.describe_launch(variant, b, h, sq, sk, d, causal, path, splits)
+
+
+def test_planning_prefill_kernels():
+    assert describe(3, 1, 32, 2048, 2048, 128, True).startswith("fa_prefill_v3_d128_2 grid=512x1x1 block=512")
+    assert describe(2, 1, 32, 2048, 2048, 128, True).startswith("fa_prefill_v2_d128_1 grid=512x1x1")
+    assert describe(1, 1, 32, 2048, 2048, 128, True).startswith("fa_prefill_v1_d128_1")
+    assert describe(2, 1, 8, 16384, 16384, 128, True).startswith("fa_prefill_v2_d128_1 grid=1024x1x1")
+    assert describe(2, 1, 16, 4096, 1024, 256, False).startswith("fa_prefill_v2_d256_1")
+    assert describe(2, 1, 1, 256, 256, 64, False).startswith("fa_prefill_v2_d64_1 grid=2x1x1")
+    for d, pad in ((1, 32), (17, 32), (33, 64), (65, 128), (129, 256), (256, 256)):
+        loader = 1 if d % 4 == 0 else 0
+        assert describe(2, 1, 1, 100, 100, d, False).startswith(f"fa_prefill_v2_d{pad}_{loader}"), d
+    assert describe(3, 1, 1, 100, 100, 17, False).startswith("fa_prefill_v3_d32_0")
+    assert describe(3, 1, 1, 100, 100, 40, False).startswith("fa_prefill_v3_d64_2")
+
+
+def test_planning_split_kv():
+    s = describe(2, 1, 32, 1, 32768, 128, False)
+    assert s.startswith("fa_decode_d128_1") and "fa_merge_d128" in s
+    assert "fa_decode" in describe(3, 1, 32, 16, 32768, 128, False)
+    assert "fa_decode" not in describe(1, 1, 32, 16, 32768, 128, False)   # v1 keeps FA-1's loop
+    assert "fa_decode" not in describe(2, 1, 32, 16, 256, 128, False)     # short keys: prefill
+    assert "fa_decode" not in describe(2, 1, 32, 16, 32768, 128, False, fa.PATH_PREFILL)
+    s = describe(2, 1, 1, 40, 300, 64, True, fa.PATH_SPLITKV, 3)
+    assert s.startswith("fa_decode_d64_1 grid=3x3x1") and "splits=3 split_len=128" in s
+
+
+def test_planning_errors():
+    with pytest.raises(fa.FaError) as e:
+        describe(2, 1, 1, 10, 10, 257, False)
+    assert e.value.status == fa.FA_ERR_UNSUPPORTED
+    with pytest.raises(fa.FaError) as e:
+        describe(1, 1, 1, 10, 1000, 64, False, fa.PATH_SPLITKV)
+    assert e.value.status == fa.FA_ERR_INVALID_ARG
+    with pytest.raises(fa.FaError) as e:
+        describe(4, 1, 1, 10, 10, 64, False)
+    assert e.value.status == fa.FA_ERR_INVALID_ARG
+    assert describe(2, 0, 1, 10, 10, 64, False) == "none"
+
+
+def test_device_entry_rejects_bad_variant_without_touching_device():
+    with pytest.raises(fa.FaError) as e:
+        fa.attention_device(7, 16, 16, 16, 1, 1, 8, 8, 16, False, 16)
+    assert e.value.status == fa.FA_ERR_INVALID_ARG
+
+
+def test_cpp_mirror_header_compiles(tmp_path):
+    hdr = os.path.join(ROOT, "flash-attention-cpu_amd", "csrc", "flash_attention.hpp")
+    src = tmp_path / "use.cpp"
+    src.write_text('#include "%s"\nint main() { flash_attention::FlashAttentionConfig c; '
+                   'return c.block_size_q == 64 ? 0 : 1; }\n' % hdr)
+    subprocess.run(["g++", "-std=c++17", "-fsyntax-only", "-I", os.path.join(ROOT, "include"), str(src)],
+                   check=True)

@@ -259,3 +259,104 @@ def test_config5c_causal_1000_remainders_d256():
         out = np.zeros(bh * s * d, dtype=np.float32)
         fa.MULTIHEAD_VARIANTS[variant](q, k, v, 1, bh, s, s, d, fa.FlashAttentionConfig(causal=True), out)
         assert_parity(out, want, f"config 5c v{variant}")
+
+
+# ---------------------------------------------------------------------------
+# Golden vectors, split-KV, device API
+# ---------------------------------------------------------------------------
+
+def test_golden_vectors():
+    from golden.make_golden import load as load_golden
+    for name, (bh, sq, sk, d, causal, q, k, v, exp) in load_golden().items():
+        want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+        for variant in ALL_VARIANTS:
+            out = np.zeros(bh * sq * d, dtype=np.float32)
+            fa.MULTIHEAD_VARIANTS[variant](q, k, v, 1, bh, sq, sk, d, fa.FlashAttentionConfig(causal=causal), out)
+            tol = 2e-5 if name.startswith("peaky") else 2e-6
+            assert max_abs_diff(out, exp) < tol, (name, variant)
+            assert_parity(out, want, f"golden {name} v{variant}")
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _device_run(variant, q, k, v, bh, sq, sk, d, causal, path=fa.PATH_AUTO, splits=0, scale=None, guard=0):
+    """Run on device tensors; `guard` floats of sentinel around the output."""
+    torch = _torch()
+    dev = torch.device("cuda", 0)
+    tq = torch.from_numpy(q).to(dev)
+    tk = torch.from_numpy(k).to(dev)
+    tv = torch.from_numpy(v).to(dev)
+    buf = torch.full((bh * sq * d + 2 * guard,), 12.5, device=dev)
+    out = buf[guard:guard + bh * sq * d]
+    fa.attention_device(variant, tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), 1, bh, sq, sk, d, causal,
+                        out.data_ptr(), torch.cuda.current_stream().cuda_stream, softmax_scale=scale, path=path,
+                        num_splits=splits)
+    torch.cuda.synchronize()
+    host = buf.cpu().numpy()
+    if guard:
+        assert np.all(host[:guard] == 12.5) and np.all(host[-guard:] == 12.5), "write outside out"
+    return host[guard:guard + bh * sq * d]
+
+
+def test_split_kv_matches_oracle_and_prefill():
+    rng = np.random.default_rng(77)
+    cases = [(1, 1, 700, 128, False), (3, 16, 1000, 128, False), (2, 5, 333, 64, True), (1, 40, 513, 32, True),
+             (2, 64, 2048, 256, False), (1, 17, 129, 17, False), (4, 1, 4096, 40, False), (1, 33, 96, 128, True)]
+    for bh, sq, sk, d, causal in cases:
+        q = rng.standard_normal(bh * sq * d, dtype=np.float32)
+        k = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        v = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+        pre = _device_run(2, q, k, v, bh, sq, sk, d, causal, fa.PATH_PREFILL, guard=64)
+        assert_parity(pre, want, f"prefill {bh},{sq},{sk},{d},{causal}")
+        for splits in (0, 1, 2, 3, 7):
+            for variant in (2, 3):
+                got = _device_run(variant, q, k, v, bh, sq, sk, d, causal, fa.PATH_SPLITKV, splits, guard=64)
+                assert_parity(got, want, f"split-kv v{variant} splits={splits} {bh},{sq},{sk},{d},{causal}")
+
+
+def test_device_api_bounds_and_determinism():
+    for bh, sq, sk, d, causal in [(3, 130, 77, 128, True), (2, 257, 300, 64, False), (1, 129, 129, 256, True),
+                                  (2, 100, 50, 20, False), (5, 3, 1000, 128, False)]:
+        q, k, v = random_vec(bh * sq * d, 1), random_vec(bh * sk * d, 2), random_vec(bh * sk * d, 3)
+        want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+        for variant in ALL_VARIANTS:
+            a = _device_run(variant, q, k, v, bh, sq, sk, d, causal, guard=256)
+            b = _device_run(variant, q, k, v, bh, sq, sk, d, causal, guard=256)
+            assert np.array_equal(a, b), f"v{variant} not deterministic"
+            assert_parity(a, want, f"device v{variant} {bh},{sq},{sk},{d},{causal}")
+
+
+def test_explicit_softmax_scale_extension():
+    bh, sq, sk, d = 2, 90, 140, 64
+    q, k, v = random_vec(bh * sq * d, 1), random_vec(bh * sk * d, 2), random_vec(bh * sk * d, 3)
+    scale = 0.3
+    # attention with scale s equals default attention on Q * (s * sqrt(d))
+    q2 = (q.astype(np.float64) * scale * np.sqrt(d)).astype(np.float32)
+    want = np.concatenate([attention_f64(q2[h * sq * d:(h + 1) * sq * d], k[h * sk * d:(h + 1) * sk * d],
+                                         v[h * sk * d:(h + 1) * sk * d], sq, sk, d, True) for h in range(bh)])
+    for variant in ALL_VARIANTS:
+        got = _device_run(variant, q, k, v, bh, sq, sk, d, True, scale=scale)
+        assert max_abs_diff(got, want) < 1e-5
+
+
+def test_long_context_config3_properties():
+    # 8 heads x 16384^2 causal: full parity against the CPU v2 on a sample of
+    # rows (float64 naive per row) plus the causal row-0 known answer.
+    bh, s, d = 8, 16384, 128
+    q, k, v = _qkv(bh, s, s, d)
+    rows = [0, 1, 127, 128, 4095, 8191, 12345, 16383]
+    for variant in (1, 2, 3):
+        out = np.zeros(bh * s * d, dtype=np.float32)
+        fa.MULTIHEAD_VARIANTS[variant](q, k, v, 1, bh, s, s, d, fa.FlashAttentionConfig(causal=True), out)
+        assert np.all(np.isfinite(out))
+        for h in (0, 7):
+            sl_q = slice(h * s * d, (h + 1) * s * d)
+            o = out[sl_q].reshape(s, d)
+            assert max_abs_diff(o[0], v[h * s * d:h * s * d + d]) < 1e-6
+            for r in rows:
+                ref = oracle.naive_f64(q[sl_q], k[sl_q], v[sl_q], s, s, d, True, r, 1)
+                assert max_abs_diff(o[r], ref) < 2e-5, (variant, h, r)
