@@ -126,10 +126,13 @@ struct Launch {
 
 struct Plan {
     bool split = false;
-    Launch first, second;   // second is the split-KV merge
+    Launch first, second;   // second: the split-KV merge
     FaParams p{};
     size_t ws_floats = 0;   // split-KV workspace (part_o + part_ml)
 };
+
+// Most splits fa_merge's LDS weight table holds.
+constexpr int kMaxSplits = 1024;
 
 int pad_d(size_t d) {
     if (d <= 32) return 32;
@@ -199,19 +202,22 @@ int make_plan(int variant, const float* q, const float* k, const float* v, const
         return FA_OK;
     }
     // Split-KV: each workgroup takes split_len keys (a multiple of 64) for one
-    // (bh, 16-row query tile); aim for ~4 workgroups per CU.
+    // (bh, 16-row query tile).  By default the split count fills exactly one
+    // round of resident workgroups (no tail), with at least 64 keys each.
     size_t nsplit;
     if (opts && opts->num_splits > 0) {
         nsplit = (size_t)opts->num_splits;
     } else {
-        const size_t target = 4 * (size_t)num_cus;
-        nsplit = target / (nqt * bh);
+        const size_t wg_per_cu = 2;   // 8 waves per CU at the decode kernel's register use
+        const size_t slots = wg_per_cu * (size_t)num_cus;
+        nsplit = slots / (nqt * bh);
         if (nsplit < 1) nsplit = 1;
+        if (nsplit > (size_t)kMaxSplits) nsplit = kMaxSplits;
     }
     size_t split_len = (sk + nsplit - 1) / nsplit;
     split_len = ((split_len + 63) / 64) * 64;
     nsplit = (sk + split_len - 1) / split_len;
-    if (nsplit > imax || split_len > imax) return FA_ERR_UNSUPPORTED;
+    if (nsplit > (size_t)kMaxSplits || split_len > imax) return FA_ERR_UNSUPPORTED;
     p.nqt = static_cast<int>(nqt);
     p.num_splits = static_cast<int>(nsplit);
     p.split_len = static_cast<int>(split_len);
@@ -223,9 +229,8 @@ int make_plan(int variant, const float* q, const float* k, const float* v, const
     plan->first.bx = 64 * kDecodeWaves;
     std::snprintf(buf, sizeof(buf), "fa_merge_d%d", D);
     plan->second.name = buf;
-    const size_t threads = bh * sq * ((d + 3) / 4);
-    plan->second.gx = static_cast<unsigned>((threads + 255) / 256);
-    plan->second.bx = 256;
+    plan->second.gx = static_cast<unsigned>(bh * sq);   // one wave per output row
+    plan->second.bx = 64;
     plan->ws_floats = bh * nqt * nsplit * (16 * (size_t)D + 32);
     return FA_OK;
 }
@@ -263,8 +268,9 @@ int run_device(int variant, hipStream_t stream, const float* q, const float* k, 
         return FA_ERR_ALLOC;
     }
     const int D = pad_d(d);
+    const size_t parts = bh * (size_t)plan.p.nqt * plan.p.num_splits;
     plan.p.part_o = ws;
-    plan.p.part_ml = ws + bh * (size_t)plan.p.nqt * plan.p.num_splits * 16 * D;
+    plan.p.part_ml = ws + parts * 16 * D;
     rc = launch(dev, plan.first, &plan.p, stream);
     if (rc == FA_OK) rc = launch(dev, plan.second, &plan.p, stream);
     if (hipFreeAsync(ws, stream) != hipSuccess) {

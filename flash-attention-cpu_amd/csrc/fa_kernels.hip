@@ -61,13 +61,18 @@ __device__ __forceinline__ float rescale_factor(float m_old, float m_new, float 
     return (m_old == FA_NEG_INF) ? 0.0f : fa_exp2((m_old - m_new) * c);
 }
 
-template <bool VEC>
+// Four floats of row `row` from column `col` (zero outside [0,nrows) x [0,d)).
+// NT: non-temporal load, for data streamed exactly once (split-KV K/V).
+template <bool VEC, bool NT = false>
 __device__ __forceinline__ f32x4 load4(const float* __restrict__ base, int row, int nrows, int col, int d) {
     f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
     if (row < nrows) {
         const float* p = base + (size_t)row * d + col;
         if (VEC) {
-            if (col < d) v = *reinterpret_cast<const f32x4*>(p);
+            if (col < d) {
+                if constexpr (NT) v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+                else v = *reinterpret_cast<const f32x4*>(p);
+            }
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
@@ -507,21 +512,27 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
 // ---------------------------------------------------------------------------
 // Split-KV decode kernel (new; no counterpart in the reference).
 //
-// For short query blocks against long key ranges: each wave takes 16 query
-// rows (zero-padded) and a contiguous key range of its split, computes
-// S^T = K Q^T on 16x16x4 MFMA straight from global memory (K and V are each
-// read once, with 128-bit loads), keeps (m, l, O) per query row, and the 4
-// waves of a workgroup merge through LDS into one partial per workgroup.
-// fa_merge then combines the partials of all splits by log-sum-exp.
+// For short query blocks against long key ranges.  Workgroup (split, qt, bh)
+// takes keys [split*split_len, +split_len) of one (batch*head) for query rows
+// 16qt .. 16qt+15 (zero-padded); its 4 waves take consecutive quarters.  A
+// wave streams its keys 16 at a time straight from HBM with 128-bit loads
+// into MFMA operand registers: S^T = K Q^T (K rows as the A operand, Q as B)
+// and O^T += V^T P^T (V as A with the 64hh + 4i + j column map), with the
+// same masked online softmax as the prefill kernel.  DBUF = true keeps two
+// register sets so block n+1 is in flight while block n computes; DBUF =
+// false re-issues each operand's loads as soon as it has been consumed.  The
+// 4 waves merge through LDS into one partial (m, l, O) per workgroup, and
+// fa_merge combines the splits by log-sum-exp.
 // ---------------------------------------------------------------------------
-template <int D, bool VEC>
+template <int D, bool VEC, bool DBUF>
 __device__ __forceinline__ void decode_body(const FaParams& p) {
     constexpr int NQ = D / 4;          // MFMA k-steps over d (16x16x4)
     constexpr int NKL = D / 16;        // 128-bit K loads per lane per 16 keys
     constexpr int NVL = D / 64 > 0 ? D / 64 : 1;  // 128-bit V loads per lane per key step
     constexpr int VW = D >= 64 ? 4 : D / 16;      // floats per lane per V load
     constexpr int NOB = D / 16;        // O^T blocks of 16 dv
-    __shared__ __attribute__((aligned(16))) float lds[4 * (NOB * 4 * 64 + 128)];
+    constexpr int WSTRIDE = NOB * 4 * 64 + 128;
+    __shared__ __attribute__((aligned(16))) float lds[3 * WSTRIDE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -544,9 +555,8 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
     const int qlast = min(seq_q, q0 + 16) - 1;
 
     // This wave's keys.
-    const int k_split0 = split * p.split_len;
     const int wave_len = p.split_len / 4;
-    int kbeg = k_split0 + wave * wave_len;
+    const int kbeg = split * p.split_len + wave * wave_len;
     int kend = min(seq_k, kbeg + wave_len);
     if (causal) kend = min(kend, qlast + 1);
 
@@ -554,7 +564,7 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
     float qreg[NQ];
 #pragma unroll
     for (int cc = 0; cc < D / 16; ++cc) {
-        f32x4 t = load4<VEC>(Qh, qrow, seq_q, 16 * cc + 4 * lg, d);
+        const f32x4 t = load4<VEC>(Qh, qrow, seq_q, 16 * cc + 4 * lg, d);
 #pragma unroll
         for (int i = 0; i < 4; ++i) qreg[4 * cc + i] = t[i];
     }
@@ -564,16 +574,18 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
     for (int j = 0; j < NOB; ++j) o[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
     float m = FA_NEG_INF, l = 0.0f;
 
-    // One 16-key block: K rows kb + lr (A operand), V rows kb + 4lg + r.
-    auto load_block = [&](int kb, f32x4* kk, f32x4* vv) {
+    // K rows kb + lr (A operand), V rows kb + 4lg + r (A operand of O^T).
+    auto load_k = [&](int kb, f32x4* kk) {
 #pragma unroll
-        for (int cc = 0; cc < NKL; ++cc) kk[cc] = load4<VEC>(Kh, kb + lr, kend, 16 * cc + 4 * lg, d);
+        for (int cc = 0; cc < NKL; ++cc) kk[cc] = load4<VEC, true>(Kh, kb + lr, kend, 16 * cc + 4 * lg, d);
+    };
+    auto load_v = [&](int kb, f32x4* vv) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int hh = 0; hh < NVL; ++hh) {
                 if constexpr (VW == 4) {
-                    vv[r * NVL + hh] = load4<VEC>(Vh, kb + 4 * lg + r, kend, 64 * hh + 4 * lr, d);
+                    vv[r * NVL + hh] = load4<VEC, true>(Vh, kb + 4 * lg + r, kend, 64 * hh + 4 * lr, d);
                 } else {
                     // D = 32: 2 floats per lane (dv = 2*lr + j)
                     f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -588,8 +600,10 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
                 }
             }
     };
-    auto compute_block = [&](int kb, const f32x4* kk, const f32x4* vv) {
-        // Blocked summation over d, 16 products (4 MFMA steps) per block.
+
+    // Scores of one 16-key block.  Blocked summation over d, 16 products
+    // (4 MFMA steps) per block.
+    auto scores = [&](int kb, const f32x4* kk) -> f32x4 {
         f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int cc = 0; cc < NKL; ++cc) {
@@ -599,15 +613,17 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
                 t = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[cc][i], qreg[4 * cc + i], t, 0, 0, 0);
             s = (cc == 0) ? t : s + t;
         }
-        // s[r] = score(key kb + 4lg + r, query qrow)
+        return s;
+    };
+    // Masked online softmax + PV for one block (s[r] = score(key kb+4lg+r, qrow)).
+    auto finish = [&](int kb, f32x4 s, const f32x4* vv) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int key = kb + 4 * lg + r;
             if (key >= kend || (causal && key > qrow)) s[r] = FA_NEG_INF;
         }
         float mt = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-        mt = fmaxf(mt, __shfl_xor(mt, 16));
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        mt = row4_max(mt);
         const float m_new = fmaxf(m, mt);
         const float m_use = (m_new == FA_NEG_INF) ? 0.0f : m_new;
         float ps = 0.0f;
@@ -632,30 +648,48 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
                                                                          o[hh * VW + j], 0, 0, 0);
     };
 
-    f32x4 ka[NKL], va[4 * NVL], kb_[NKL], vb_[4 * NVL];
-    int kb = kbeg;
-    if (kb < kend) load_block(kb, ka, va);
-    while (kb < kend) {
-        const int kn = kb + 16;
-        if (kn < kend) load_block(kn, kb_, vb_);
-        compute_block(kb, ka, va);
-        kb = kn;
-        if (kb >= kend) break;
-        const int kn2 = kb + 16;
-        if (kn2 < kend) load_block(kn2, ka, va);
-        compute_block(kb, kb_, vb_);
-        kb = kn2;
+    if constexpr (DBUF) {
+        f32x4 ka[NKL], va[4 * NVL], kb2[NKL], vb2[4 * NVL];
+        int kb = kbeg;
+        if (kb < kend) {
+            load_k(kb, ka);
+            load_v(kb, va);
+        }
+        while (kb < kend) {
+            if (kb + 16 < kend) {
+                load_k(kb + 16, kb2);
+                load_v(kb + 16, vb2);
+            }
+            finish(kb, scores(kb, ka), va);
+            kb += 16;
+            if (kb >= kend) break;
+            if (kb + 16 < kend) {
+                load_k(kb + 16, ka);
+                load_v(kb + 16, va);
+            }
+            finish(kb, scores(kb, kb2), vb2);
+            kb += 16;
+        }
+    } else {
+        f32x4 kk[NKL], vv[4 * NVL];
+        if (kbeg < kend) {
+            load_k(kbeg, kk);
+            load_v(kbeg, vv);
+        }
+        for (int kb = kbeg; kb < kend; kb += 16) {
+            const bool more = kb + 16 < kend;
+            const f32x4 s = scores(kb, kk);
+            if (more) load_k(kb + 16, kk);   // K registers are free again
+            finish(kb, s, vv);
+            if (more) load_v(kb + 16, vv);   // V registers are free again
+        }
     }
 
-    // Row sums over the 4 lane groups.
-    l = l + __shfl_xor(l, 16);
-    l = l + __shfl_xor(l, 32);
+    l = row4_sum(l);
 
-    // Merge the 4 waves through LDS: wave w writes, wave 0 combines.
-    float* mb = lds;
-    constexpr int WSTRIDE = NOB * 4 * 64 + 128;
+    // Merge the 4 waves through LDS: waves 1..3 write, wave 0 combines.
     if (wave != 0) {
-        float* w = mb + (wave - 1) * WSTRIDE;
+        float* w = lds + (wave - 1) * WSTRIDE;
 #pragma unroll
         for (int j = 0; j < NOB; ++j)
 #pragma unroll
@@ -669,7 +703,7 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
     float mn = m;
 #pragma unroll
     for (int w = 0; w < 3; ++w) {
-        mw[w] = mb[w * WSTRIDE + NOB * 4 * 64 + lane];
+        mw[w] = lds[w * WSTRIDE + NOB * 4 * 64 + lane];
         mn = fmaxf(mn, mw[w]);
     }
     const float mu = (mn == FA_NEG_INF) ? 0.0f : mn;
@@ -680,13 +714,12 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
 #pragma unroll
     for (int w = 0; w < 3; ++w) {
         const float cw = rescale_factor(mw[w], mu, c);
-        l += mb[w * WSTRIDE + NOB * 4 * 64 + 64 + lane] * cw;
+        l += lds[w * WSTRIDE + NOB * 4 * 64 + 64 + lane] * cw;
 #pragma unroll
         for (int j = 0; j < NOB; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) o[j][r] += mb[w * WSTRIDE + (j * 4 + r) * 64 + lane] * cw;
+            for (int r = 0; r < 4; ++r) o[j][r] += lds[w * WSTRIDE + (j * 4 + r) * 64 + lane] * cw;
     }
-
     // Partial for (bh, qt, split): O rows (unnormalised), m and l per query.
     const size_t pidx = ((size_t)bh * p.nqt + qt) * p.num_splits + split;
     float* po = p.part_o + pidx * 16 * D;
@@ -702,7 +735,7 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
         for (int r = 0; r < 4; ++r) {
             const int dv0 = 64 * hh + VW * (4 * lg + r);
             if constexpr (VW == 4) {
-                f32x4 t = {o[hh * 4 + 0][r], o[hh * 4 + 1][r], o[hh * 4 + 2][r], o[hh * 4 + 3][r]};
+                const f32x4 t = {o[hh * 4 + 0][r], o[hh * 4 + 1][r], o[hh * 4 + 2][r], o[hh * 4 + 3][r]};
                 *reinterpret_cast<f32x4*>(po + lr * D + dv0) = t;
             } else {
 #pragma unroll
@@ -711,38 +744,60 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
         }
 }
 
-// Combine split partials: O = sum_s 2^((m_s - M) c) O_s / sum_s 2^((m_s - M) c) l_s.
-// One thread per (bh, query, 4 consecutive dv).
-__device__ __forceinline__ void merge_body(const FaParams& p, int D) {
-    const int seq_q = p.seq_q, d = p.d;
-    const int nchunk = (d + 3) / 4;
-    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const size_t total = (size_t)p.bh * seq_q * nchunk;
-    if (gid >= total) return;
-    const int chunk = (int)(gid % nchunk);
-    const size_t row = gid / nchunk;           // bh * seq_q + q
-    const int q = (int)(row % seq_q);
-    const int bh = (int)(row / seq_q);
+// Combine the split partials of one query row (one wave per row):
+// O = sum_s 2^((m_s - M) c) O_s / sum_s 2^((m_s - M) c) l_s, where empty
+// splits (m_s = -inf, l_s = 0) weigh 0.
+template <int D>
+__device__ __forceinline__ void merge_body(const FaParams& p) {
+    constexpr int CH = D / 4;                // 4-float column chunks per row
+    constexpr int GROUPS = 64 / CH > 0 ? 64 / CH : 1;   // lanes sharing a chunk split the splits
+    __shared__ float wts[1024];
+    __shared__ __attribute__((aligned(16))) float part[64 * 4];
+
+    const int lane = threadIdx.x;
+    const int row = blockIdx.x;              // bh * seq_q + q
+    const int q = row % p.seq_q, bh = row / p.seq_q;
     const int qt = q / 16, qi = q % 16;
+    const int ns = p.num_splits;
     const float c = p.scale_log2e;
-    const size_t pbase = ((size_t)bh * p.nqt + qt) * p.num_splits;
+    const size_t pbase = ((size_t)bh * p.nqt + qt) * ns;
+
     float M = FA_NEG_INF;
-    for (int s = 0; s < p.num_splits; ++s) M = fmaxf(M, p.part_ml[(pbase + s) * 32 + qi]);
+    for (int sp = lane; sp < ns; sp += 64) M = fmaxf(M, p.part_ml[(pbase + sp) * 32 + qi]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
     const float Mu = (M == FA_NEG_INF) ? 0.0f : M;
     float L = 0.0f;
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int s = 0; s < p.num_splits; ++s) {
-        const float* ml = p.part_ml + (pbase + s) * 32;
+    for (int sp = lane; sp < ns; sp += 64) {
+        const float* ml = p.part_ml + (pbase + sp) * 32;
         const float w = rescale_factor(ml[qi], Mu, c);
+        wts[sp] = w;
         L += ml[16 + qi] * w;
-        const f32x4 v = *reinterpret_cast<const f32x4*>(p.part_o + ((pbase + s) * 16 + qi) * D + 4 * chunk);
-        acc += v * w;
     }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off);
+    __syncthreads();
+
+    const int ch = lane % CH, grp = lane / CH;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (grp < GROUPS) {
+        const float* po = p.part_o + (pbase * 16 + qi) * D + 4 * ch;
+#pragma unroll 8
+        for (int sp = grp; sp < ns; sp += GROUPS)
+            acc += *reinterpret_cast<const f32x4*>(po + (size_t)sp * 16 * D) * wts[sp];
+    }
+    if constexpr (GROUPS > 1) {
+        *reinterpret_cast<f32x4*>(part + 4 * lane) = acc;
+        __syncthreads();
+        if (grp != 0) return;
+        for (int g2 = 1; g2 < GROUPS; ++g2) acc += *reinterpret_cast<const f32x4*>(part + 4 * (g2 * CH + ch));
+    }
+    if (lane >= CH) return;
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    float* orow = p.out + row * d;
+    float* orow = p.out + (size_t)row * p.d;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-        if (4 * chunk + e < d) orow[4 * chunk + e] = acc[e] * inv;
+        if (4 * ch + e < p.d) orow[4 * ch + e] = acc[e] * inv;
 }
 
 // ---------------------------------------------------------------------------
@@ -767,19 +822,27 @@ FA_PREFILL_ALL(64)
 FA_PREFILL_ALL(128)
 FA_PREFILL_ALL(256)
 
-#define FA_DECODE(D, VEC) \
-    extern "C" __global__ void __launch_bounds__(256, 2) fa_decode_d##D##_##VEC(FaParams p) { decode_body<D, VEC != 0>(p); }
-FA_DECODE(32, 1)
-FA_DECODE(32, 0)
-FA_DECODE(64, 1)
-FA_DECODE(64, 0)
-FA_DECODE(128, 1)
-FA_DECODE(128, 0)
-FA_DECODE(256, 1)
-FA_DECODE(256, 0)
+// Decode register double-buffering (FA_DECODE_DBUF=1) trades occupancy for
+// one block of loads in flight per register set.
+#ifndef FA_DECODE_DBUF
+#define FA_DECODE_DBUF 1
+#endif
+#define FA_DECODE(D, VEC, OCC1, OCC2)                                                            \
+    extern "C" __global__ void __launch_bounds__(256, FA_DECODE_DBUF ? OCC2 : OCC1)              \
+        fa_decode_d##D##_##VEC(FaParams p) {                                                     \
+        decode_body<D, VEC != 0, FA_DECODE_DBUF != 0>(p);                                        \
+    }
+FA_DECODE(32, 1, 4, 4)
+FA_DECODE(32, 0, 4, 4)
+FA_DECODE(64, 1, 4, 3)
+FA_DECODE(64, 0, 4, 3)
+FA_DECODE(128, 1, 3, 2)
+FA_DECODE(128, 0, 3, 2)
+FA_DECODE(256, 1, 2, 2)
+FA_DECODE(256, 0, 2, 2)
 
 #define FA_MERGE(D) \
-    extern "C" __global__ void __launch_bounds__(256) fa_merge_d##D(FaParams p) { merge_body(p, D); }
+    extern "C" __global__ void __launch_bounds__(64) fa_merge_d##D(FaParams p) { merge_body<D>(p); }
 FA_MERGE(32)
 FA_MERGE(64)
 FA_MERGE(128)

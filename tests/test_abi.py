@@ -172,7 +172,8 @@ def test_planning_prefill_kernels():
 
 def test_planning_split_kv():
     s = describe(2, 1, 32, 1, 32768, 128, False)
-    assert s.startswith("fa_decode_d128_1") and "fa_merge_d128" in s
+    assert s.startswith("fa_decode_d128_1 grid=16x1x32") and "fa_merge_d128 grid=32x1x1 block=64" in s
+    assert "splits=16 split_len=2048" in s
     assert "fa_decode" in describe(3, 1, 32, 16, 32768, 128, False)
     assert "fa_decode" not in describe(1, 1, 32, 16, 32768, 128, False)   # v1 keeps FA-1's loop
     assert "fa_decode" not in describe(2, 1, 32, 16, 256, 128, False)     # short keys: prefill
