@@ -32,7 +32,6 @@ namespace {
 
 constexpr int kMaxDevices = 64;
 constexpr int kMaxD = 256;
-constexpr int kPrefillRows = 128;   // query rows per prefill workgroup
 constexpr int kDecodeRows = 16;     // query rows per split-KV wave
 constexpr int kDecodeWaves = 4;     // waves per split-KV workgroup
 
@@ -173,7 +172,8 @@ int make_plan(int variant, const float* q, const float* k, const float* v, const
     p.causal = causal ? 1 : 0;
     p.scale_log2e = scale * 1.44269504088896341f;
 
-    const size_t nqb = (sq + kPrefillRows - 1) / kPrefillRows;
+    const size_t rows = (size_t)fa_prefill_rows(D);   // query rows per prefill workgroup
+    const size_t nqb = (sq + rows - 1) / rows;
     const size_t nqt = (sq + kDecodeRows - 1) / kDecodeRows;
     bool split = false;
     if (variant != 1) {
@@ -197,7 +197,7 @@ int make_plan(int variant, const float* q, const float* k, const float* v, const
         std::snprintf(buf, sizeof(buf), "fa_prefill_v%d_d%d_%d", variant, D, loader);
         plan->first.name = buf;
         plan->first.gx = static_cast<unsigned>(nqb * bh);
-        plan->first.bx = 512;
+        plan->first.bx = 64 * fa_prefill_waves(D);
         plan->ws_floats = 0;
         return FA_OK;
     }

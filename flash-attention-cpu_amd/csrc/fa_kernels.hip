@@ -104,9 +104,9 @@ __device__ __forceinline__ void map_block(const FaParams& p, int& qb, int& bh) {
 // ---------------------------------------------------------------------------
 // Prefill kernel: one template for v1 / v2 / v3.
 //
-// A workgroup of 8 waves owns BQ = 128 query rows of one (batch*head)
+// A workgroup of NW waves owns BQ = 16*NW query rows of one (batch*head)
 // slice; wave w owns rows 16w .. 16w+15.  Keys stream through LDS in stages
-// of SK keys (64 for d <= 128, 32 for d = 256) shared by all 8 waves.
+// of SK keys shared by the workgroup's waves (fa_params.h: fa_prefill_*).
 //
 // Scores are computed transposed on 16x16x4 f32 MFMA, S^T = K Q^T: A = 16 K
 // rows from LDS, B = the wave's 16 Q rows held in VGPRs.  Lane l then owns
@@ -118,19 +118,25 @@ __device__ __forceinline__ void map_block(const FaParams& p, int& qb, int& bh) {
 // 64 output columns: lane l reads V[key][64hh + 4(l%16) .. +3], so O^T block
 // (hh, j) row i holds dv = 64hh + 4i + j.
 //
-// LDS holds K and V stages as rows of D + 4 floats: the 16-byte pad shifts
-// consecutive rows by 4 banks, so the row-per-lane K reads and the
-// contiguous V reads are conflict-free, and every read address is a
-// per-lane base plus an immediate offset.  The gfx950 global->LDS DMA
-// writes 1 KB runs of this padded image; pad slots re-load a valid chunk.
+// LDS holds K and V stages as padded rows: K rows of D + 8 floats, so the 32
+// lanes a 128-bit read serves per cycle (16 rows x 2 adjacent chunks) hit 32
+// distinct 4-bank groups of the 128 banks; V rows of D + 16 floats (D + 8
+// for D = 32), so the 4 rows read together (4 lane groups x 16 contiguous
+// chunks) sit 256 B apart modulo the bank width.  Every read address is a
+// per-lane base plus an immediate offset.  The gfx950 global->LDS DMA writes
+// 1 KB runs of this padded image; pad slots re-load a valid chunk.
 //
 // LOADER: 0 = scalar global loads through VGPRs (any d), 1 = 128-bit loads
 // through VGPRs (d % 4 == 0), 2 = global_load_lds_dwordx4 DMA (d % 4 == 0,
 // 16-byte aligned operands; v3 only).
 // ---------------------------------------------------------------------------
-template <int D>
+// Padded LDS row lengths (floats) of the K and V stage images.
+template <int D> constexpr int kpad_row() { return D + 8; }
+template <int D> constexpr int vpad_row() { return D == 32 ? D + 8 : D + 16; }
+
+template <int LD>
 __device__ __forceinline__ int lds_off(int row, int chunk) {
-    return row * (D + 4) + 4 * chunk;
+    return row * LD + 4 * chunk;
 }
 
 template <int N>
@@ -158,10 +164,10 @@ __device__ __forceinline__ float row4_sum(float x) {
 
 template <int D, int VARIANT, int LOADER>
 __device__ __forceinline__ void prefill_body(const FaParams& p) {
-    constexpr int NW = 8;                     // waves per workgroup
+    constexpr int NW = fa_prefill_waves(D);   // waves per workgroup
     constexpr int NT = NW * 64;               // threads
-    constexpr int BQ = 128;                   // query rows per workgroup
-    constexpr int SK = (D <= 128) ? 64 : 32;  // keys per LDS stage
+    constexpr int BQ = fa_prefill_rows(D);    // query rows per workgroup
+    constexpr int SK = fa_prefill_stage_keys(D);   // keys per LDS stage
     constexpr int KB = SK / 16;               // 16-key blocks per stage
     constexpr int NQ = D / 4;                 // MFMA k-steps over d
     constexpr int NC = D / 16;                // 128-bit K reads per lane per key block
@@ -169,8 +175,10 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     constexpr int NVR = (D >= 64) ? D / 64 : 1;   // V reads per key
     constexpr int NOB = D / 16;               // O^T accumulator blocks
     constexpr int CPR = D / 4;                // 16-byte chunks per row
-    constexpr int LDK = D + 4;                // padded LDS row (floats)
-    constexpr int TILE = SK * LDK;            // floats per K (or V) stage
+    constexpr int LDK = kpad_row<D>();        // padded K row (floats)
+    constexpr int LDV = vpad_row<D>();        // padded V row (floats)
+    constexpr int KTILE = SK * LDK;           // floats per K stage
+    constexpr int VTILE = SK * LDV;           // floats per V stage
     constexpr bool DMA = (LOADER == 2);
     constexpr int NBUF = (VARIANT == 3) ? 2 : 1;
     static_assert(NVR * VW == NOB, "V read layout");
@@ -179,10 +187,10 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
 
     // Separate arrays so the compiler can tell a DMA in flight into one
     // buffer from LDS reads of another (no needless vmcnt waits).
-    __shared__ __attribute__((aligned(16))) float Kb0[TILE];
-    __shared__ __attribute__((aligned(16))) float Vb0[TILE];
-    __shared__ __attribute__((aligned(16))) float Kb1[NBUF > 1 ? TILE : 4];
-    __shared__ __attribute__((aligned(16))) float Vb1[NBUF > 1 ? TILE : 4];
+    __shared__ __attribute__((aligned(16))) float Kb0[KTILE];
+    __shared__ __attribute__((aligned(16))) float Vb0[VTILE];
+    __shared__ __attribute__((aligned(16))) float Kb1[NBUF > 1 ? KTILE : 4];
+    __shared__ __attribute__((aligned(16))) float Vb1[NBUF > 1 ? VTILE : 4];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -234,21 +242,23 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             rg[it] = load4<LOADER != 0>(src, kbase + idx / CPR, seq_k, 4 * (idx % CPR), d);
         }
     };
-    auto store_regs = [&](float* dst, const f32x4* rg) {
+    auto store_regs = [&](auto ld, float* dst, const f32x4* rg) {
+        constexpr int LD = decltype(ld)::value;
 #pragma unroll
         for (int it = 0; it < LOAD_ITERS; ++it) {
             const int idx = tid + it * NT;
-            *reinterpret_cast<f32x4*>(dst + lds_off<D>(idx / CPR, idx % CPR)) = rg[it];
+            *reinterpret_cast<f32x4*>(dst + lds_off<LD>(idx / CPR, idx % CPR)) = rg[it];
         }
     };
-    // DMA: the stage image is SK rows of CPR + 1 chunks (the last one is the
+    // DMA: the stage image is SK rows of LD/4 chunks (the last ones are the
     // pad); run R = i*NW + w (64 chunks = 1 KB) is written by wave w, lane L
     // fetching the global chunk that belongs at image position 64R + L.
     // Rows past seq_k are clamped to a real row (masked to -inf / multiplied
     // by 0 later), columns past d and pad slots to column 0, so every read
     // is in bounds.
-    auto dma_stage = [&](const float* __restrict__ src, int kbase, float* dst) {
-        constexpr int TOTAL = SK * (CPR + 1);
+    auto dma_stage = [&](auto ld, const float* __restrict__ src, int kbase, float* dst) {
+        constexpr int RCH = decltype(ld)::value / 4;   // chunks per padded row
+        constexpr int TOTAL = SK * RCH;
         constexpr int RUNS = (TOTAL + 63) / 64;
         constexpr int NI = (RUNS + NW - 1) / NW;
 #pragma unroll
@@ -256,7 +266,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             const int run = i * NW + wave;
             if (run < RUNS) {
                 const int pos = run * 64 + lane;
-                const int r = pos / (CPR + 1), cidx = pos % (CPR + 1);
+                const int r = pos / RCH, cidx = pos % RCH;
                 const int key = min(kbase + r, seq_k - 1);
                 const int col = (cidx < CPR && 4 * cidx < d) ? 4 * cidx : 0;
                 if (pos < TOTAL)
@@ -264,15 +274,17 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             }
         }
     };
-    auto fill_stage = [&](const float* __restrict__ src, int kbase, float* dst) {
+    auto fill_stage = [&](auto ld, const float* __restrict__ src, int kbase, float* dst) {
         if constexpr (DMA) {
-            dma_stage(src, kbase, dst);
+            dma_stage(ld, src, kbase, dst);
         } else {
             f32x4 rg[LOAD_ITERS];
             load_regs(src, kbase, rg);
-            store_regs(dst, rg);
+            store_regs(ld, dst, rg);
         }
     };
+    const std::integral_constant<int, LDK> KL{};
+    const std::integral_constant<int, LDV> VL{};
 
     // ---- stage math ---------------------------------------------------------
     // S^T for the stage's KB key blocks from `Ks`.  Blocked summation over
@@ -286,14 +298,14 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         // the live set to two chunks' reads.
         f32x4 kk[2][KB];
 #pragma unroll
-        for (int b = 0; b < KB; ++b) kk[0][b] = *reinterpret_cast<const f32x4*>(Ks + lds_off<D>(16 * b + li, g));
+        for (int b = 0; b < KB; ++b) kk[0][b] = *reinterpret_cast<const f32x4*>(Ks + lds_off<LDK>(16 * b + li, g));
 #pragma unroll
         for (int cc = 0; cc < NC; ++cc) {
             if (cc + 1 < NC) {
 #pragma unroll
                 for (int b = 0; b < KB; ++b)
                     kk[(cc + 1) & 1][b] =
-                        *reinterpret_cast<const f32x4*>(Ks + lds_off<D>(16 * b + li, 4 * (cc + 1) + g));
+                        *reinterpret_cast<const f32x4*>(Ks + lds_off<LDK>(16 * b + li, 4 * (cc + 1) + g));
             }
 #pragma unroll
             for (int b = 0; b < KB; ++b) {
@@ -363,9 +375,9 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
 #pragma unroll
             for (int hh = 0; hh < NVR; ++hh) {
                 if constexpr (VW == 4) {
-                    vv[hh] = *reinterpret_cast<const f32x4*>(Vs + lds_off<D>(kr, 16 * hh + li));
+                    vv[hh] = *reinterpret_cast<const f32x4*>(Vs + lds_off<LDV>(kr, 16 * hh + li));
                 } else {
-                    const f32x2 t = *reinterpret_cast<const f32x2*>(Vs + lds_off<D>(kr, li >> 1) + 2 * (li & 1));
+                    const f32x2 t = *reinterpret_cast<const f32x2*>(Vs + lds_off<LDV>(kr, li >> 1) + 2 * (li & 1));
                     vv[hh] = (f32x4){t[0], t[1], 0.0f, 0.0f};
                 }
             }
@@ -413,9 +425,9 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         // is issued right after stage st's softmax + PV, and one barrier
         // closes the step.  The loop is unrolled by two so every buffer is a
         // compile-time choice.
-        fill_stage(Kh, 0, Kb0);
-        if (nst > 1) fill_stage(Kh, SK, Kb1);
-        fill_stage(Vh, 0, Vb0);
+        fill_stage(KL, Kh, 0, Kb0);
+        if (nst > 1) fill_stage(KL, Kh, SK, Kb1);
+        fill_stage(VL, Vh, 0, Vb0);
         wait_vmcnt<0>();
         __syncthreads();
         f32x4 s_cur[KB];
@@ -432,8 +444,8 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             const float* k_next = P ? Kb0 : Kb1;  // K(st+1)
             const float* v_cur = P ? Vb1 : Vb0;   // V(st)
             const bool has_next = st + 1 < nst;
-            if (st + 2 < nst) fill_stage(Kh, (st + 2) * SK, k_fill);
-            if (has_next) fill_stage(Vh, (st + 1) * SK, v_fill);
+            if (st + 2 < nst) fill_stage(KL, Kh, (st + 2) * SK, k_fill);
+            if (has_next) fill_stage(VL, Vh, (st + 1) * SK, v_fill);
             const bool act_nxt = has_next && stage_active(st + 1);
             // This stage's softmax + PV, then the next stage's QK^T from the
             // other buffer, with no barrier between them: the second wave on
@@ -460,8 +472,8 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             load_regs(Vh, 0, vr);
         }
         for (int st = 0; st < nst; ++st) {
-            store_regs(Kb0, kr);
-            store_regs(Vb0, vr);
+            store_regs(KL, Kb0, kr);
+            store_regs(VL, Vb0, vr);
             __syncthreads();
             if (st + 1 < nst) {
                 load_regs(Kh, (st + 1) * SK, kr);
@@ -805,7 +817,8 @@ __device__ __forceinline__ void merge_body(const FaParams& p) {
 // ---------------------------------------------------------------------------
 // fa_prefill_v{V}_d{D}_{L}: L = 0 scalar loads, 1 vector loads, 2 LDS DMA (v3).
 #define FA_PREFILL(D, VAR, LD)                                                                   \
-    extern "C" __global__ void __launch_bounds__(512, 1) fa_prefill_v##VAR##_d##D##_##LD(FaParams p) { \
+    extern "C" __global__ void __launch_bounds__(64 * fa_prefill_waves(D), 8 / fa_prefill_waves(D))   \
+        fa_prefill_v##VAR##_d##D##_##LD(FaParams p) {                                                \
         prefill_body<D, VAR, LD>(p);                                                             \
     }
 #define FA_PREFILL_ALL(D)  \

@@ -26,4 +26,17 @@ typedef struct FaParams {
     int split_len;       // split-KV: keys per split (multiple of 64)
 } FaParams;
 
+
+// Prefill geometry shared by the host planner and the kernels: waves per
+// workgroup (each wave owns 16 query rows) and keys per LDS stage.
+// FA_PREFILL_WAVES selects the workgroup size for d_head <= 128.
+#ifndef FA_PREFILL_WAVES
+#define FA_PREFILL_WAVES 8
+#endif
+#ifdef __cplusplus
+constexpr int fa_prefill_waves(int D) { return D <= 128 ? FA_PREFILL_WAVES : 8; }
+constexpr int fa_prefill_rows(int D) { return 16 * fa_prefill_waves(D); }
+constexpr int fa_prefill_stage_keys(int D) { return D <= 128 ? (fa_prefill_waves(D) == 8 ? 64 : 32) : 32; }
+#endif
+
 #endif

@@ -28,7 +28,9 @@ from dataclasses import dataclass
 import numpy as np
 
 _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(_PKG_DIR, "libfa_hip.so")
+# FA_HIP_LIBRARY overrides the library (e.g. a build with other tuning macros);
+# the code object is found next to it unless FA_HIP_MODULE names one.
+LIB_PATH = os.environ.get("FA_HIP_LIBRARY") or os.path.join(_PKG_DIR, "libfa_hip.so")
 MODULE_PATH = os.path.join(_PKG_DIR, "fa_kernels.hsaco")
 
 FA_OK = 0
