@@ -20,6 +20,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -199,6 +200,78 @@ int make_plan(int variant, const float* q, const float* k, const float* v, const
         plan->first.gx = static_cast<unsigned>(nqb * bh);
         plan->first.bx = 64 * fa_prefill_waves(D);
         plan->ws_floats = 0;
+        // Key split for v2/v3 when the grid would leave CUs idle: a query
+        // block's keys are cut into splits of `per` stages, one workgroup
+        // each, whose partials fa_merge combines.  Causal blocks differ in
+        // length, so `per` is chosen to minimise the estimated makespan in
+        // key-steps: rounds of resident workgroups (one per CU) x (keys per
+        // split + kOverheadKeys for loading Q and writing the partial), plus
+        // kOverheadKeys per round for the merge's re-read; at least four
+        // stages per split.  Measured on MI355X, a single round of long
+        // splits beats several rounds of short ones.  The grid lists only
+        // workgroups with keys.
+        size_t per = 0;
+        if (variant != 1) {
+            const size_t SKs = (size_t)fa_prefill_stage_keys(D, variant);
+            auto block_stages = [&](size_t b) {
+                const size_t kend = causal ? std::min(sk, (b + 1) * rows) : sk;
+                return (kend + SKs - 1) / SKs;
+            };
+            const size_t max_st = block_stages(nqb - 1);   // causal key ends grow with the block
+            auto wgs_for = [&](size_t pp) {
+                size_t n = 0;
+                for (size_t b = 0; b < nqb; ++b) n += (block_stages(b) + pp - 1) / pp;
+                return n * bh;
+            };
+            constexpr double kOverheadKeys = 48.0;
+            if (opts && opts->num_splits > 1 && path == FA_PATH_PREFILL) {
+                if (opts->num_splits > kMaxSplits) return FA_ERR_UNSUPPORTED;
+                per = (max_st + opts->num_splits - 1) / opts->num_splits;
+            } else if (path == FA_PATH_AUTO && nqb * bh < (size_t)num_cus) {
+                const double cus = (double)num_cus, skd = (double)SKs;
+                double best = std::ceil((double)(nqb * bh) / cus) * (double)max_st * skd;   // no split
+                // Candidates: for R = 1..4 rounds, the shortest split whose
+                // workgroups fit in R rounds (workgroup count falls as `per`
+                // grows, so bisect).
+                for (size_t R = 1; R <= 4; ++R) {
+                    const size_t slots = R * (size_t)num_cus;
+                    size_t lo = 4, hi = max_st;
+                    if (lo > hi || wgs_for(hi) > slots) continue;
+                    while (lo < hi) {
+                        const size_t mid = (lo + hi) / 2;
+                        if (wgs_for(mid) <= slots) hi = mid;
+                        else lo = mid + 1;
+                    }
+                    const size_t pp = lo;
+                    const double n = (double)wgs_for(pp);
+                    const double cost = std::ceil(n / cus) * ((double)pp * skd + kOverheadKeys) + n / cus * kOverheadKeys;
+                    if (cost < best) {
+                        best = cost;
+                        per = pp;
+                    }
+                }
+            }
+            if (per > 0 && (max_st + per - 1) / per < 2) per = 0;
+            if (per > 0 && (bh * sq > imax || per * SKs > imax)) return FA_ERR_UNSUPPORTED;
+            if (per > 0) {
+                const size_t nks = (max_st + per - 1) / per;
+                if (nks > 65535 || nks > (size_t)kMaxSplits) return FA_ERR_UNSUPPORTED;
+                plan->split = true;
+                p.nqt = static_cast<int>(nqt);
+                p.num_splits = static_cast<int>(nks);
+                p.split_len = static_cast<int>(per * SKs);
+                p.ks_rows = static_cast<int>(rows);
+                size_t wgs = 0;   // compact grid: split y of every block that reaches it
+                for (size_t y = 0; y < nks; ++y) wgs += (causal ? nqb - std::min(nqb, y * per * SKs / rows) : nqb) * bh;
+                if (wgs > imax) return FA_ERR_UNSUPPORTED;
+                plan->first.gx = static_cast<unsigned>(wgs);
+                std::snprintf(buf, sizeof(buf), "fa_merge_d%d", D);
+                plan->second.name = buf;
+                plan->second.gx = static_cast<unsigned>(bh * sq);   // one wave per output row
+                plan->second.bx = 64;
+                plan->ws_floats = bh * nqt * nks * (16 * (size_t)D + 32);
+            }
+        }
         return FA_OK;
     }
     // Split-KV: each workgroup takes split_len keys (a multiple of 64) for one
@@ -496,10 +569,13 @@ int fa_describe_launch(int variant, size_t batch, size_t heads, size_t sq, size_
                           plan.first.gy, plan.first.gz, plan.first.bx);
             text = tmp;
             if (plan.split) {
-                std::snprintf(tmp, sizeof(tmp), "; %s grid=%ux%ux%u block=%u; splits=%d split_len=%d",
-                              plan.second.name.c_str(), plan.second.gx, plan.second.gy, plan.second.gz,
-                              plan.second.bx, plan.p.num_splits, plan.p.split_len);
+                std::snprintf(tmp, sizeof(tmp), "; %s grid=%ux%ux%u block=%u; splits=%d", plan.second.name.c_str(),
+                              plan.second.gx, plan.second.gy, plan.second.gz, plan.second.bx, plan.p.num_splits);
                 text += tmp;
+                if (plan.p.split_len > 0) {
+                    std::snprintf(tmp, sizeof(tmp), " split_len=%d", plan.p.split_len);
+                    text += tmp;
+                }
             }
         }
     }

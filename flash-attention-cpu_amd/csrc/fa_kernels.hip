@@ -86,8 +86,7 @@ __device__ __forceinline__ f32x4 load4(const float* __restrict__ base, int row, 
 // (greedy longest-processing-time order as workgroups retire) and, when bh is
 // a multiple of 8, all blocks of one head on the same XCD (workgroups are
 // dispatched round-robin over the 8 XCDs) so its K/V stays in one L2.
-__device__ __forceinline__ void map_block(const FaParams& p, int& qb, int& bh) {
-    const int x = blockIdx.x;
+__device__ __forceinline__ void map_block(const FaParams& p, int x, int& qb, int& bh) {
     int rank;
     if (p.bh % 8 == 0) {
         const int hpx = p.bh / 8;
@@ -99,6 +98,23 @@ __device__ __forceinline__ void map_block(const FaParams& p, int& qb, int& bh) {
         rank = x / p.bh;
     }
     qb = p.causal ? (p.nqb - 1 - rank) : rank;
+}
+
+// Key-split grid: a compact 1-D list of the workgroups that have keys to
+// process (a grid padded with idle workgroups lets the dispatcher queue
+// working ones behind busy CUs).  Row y holds split y of every query block
+// whose key range reaches y * split_len -- causal blocks qb >= floor(y *
+// split_len / ks_rows), all blocks otherwise -- in map_block's order.
+__device__ __forceinline__ void map_block_split(const FaParams& p, int& qb, int& bh, int& y) {
+    int t = blockIdx.x;
+    int cnt = p.nqb;
+    for (y = 0;; ++y) {
+        cnt = p.causal ? p.nqb - (int)(((long long)y * p.split_len) / p.ks_rows) : p.nqb;
+        if (t < cnt * p.bh || y + 1 >= p.num_splits) break;
+        t -= cnt * p.bh;
+    }
+    // rank r of this row is block nqb-1-r (causal) or r, as in map_block
+    map_block(p, t, qb, bh);
 }
 
 // ---------------------------------------------------------------------------
@@ -167,7 +183,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     constexpr int NW = fa_prefill_waves(D);   // waves per workgroup
     constexpr int NT = NW * 64;               // threads
     constexpr int BQ = fa_prefill_rows(D);    // query rows per workgroup
-    constexpr int SK = fa_prefill_stage_keys(D);   // keys per LDS stage
+    constexpr int SK = fa_prefill_stage_keys(D, VARIANT);   // keys per LDS stage
     constexpr int KB = SK / 16;               // 16-key blocks per stage
     constexpr int NQ = D / 4;                 // MFMA k-steps over d
     constexpr int NC = D / 16;                // 128-bit K reads per lane per key block
@@ -198,8 +214,10 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     const int g = lane >> 4;                  // lane group 0..3
     const int li = lane & 15;
 
-    int qb, bh;
-    map_block(p, qb, bh);
+    const bool splitk = p.part_o != nullptr;
+    int qb, bh, ysplit = 0;
+    if (splitk) map_block_split(p, qb, bh, ysplit);
+    else map_block(p, blockIdx.x, qb, bh);
     const int seq_q = p.seq_q, seq_k = p.seq_k, d = p.d;
     const int q0 = qb * BQ;
     const float* __restrict__ Qh = p.q + (size_t)bh * seq_q * d;
@@ -231,7 +249,16 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     // (src/v2.rs:208-212, src/v3.rs:396-410).
     int kend = seq_k;
     if (VARIANT != 1 && causal) kend = min(seq_k, q0 + BQ);
-    const int nst = (kend + SK - 1) / SK;
+    // Key split (v2/v3 on grids smaller than the GPU): the workgroup for
+    // split y takes the split_len keys from y * split_len of its block's
+    // range and writes a partial (m, l, O) that fa_merge combines.
+    int sbeg = 0, nst = (kend + SK - 1) / SK;
+    if (splitk) {
+        const int per = p.split_len / SK;
+        sbeg = ysplit * per;              // < nst by construction of the grid
+        nst = min(nst, sbeg + per) - sbeg;
+    }
+    const int k0 = sbeg * SK;                 // first key of this workgroup
 
     // ---- stage loaders ------------------------------------------------------
     constexpr int LOAD_ITERS = (SK * CPR) / NT;
@@ -411,7 +438,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     // Is this wave's share of stage `st` worth computing?  v2/v3 skip stages
     // entirely in the future of every row of the wave; v1 does not.
     auto stage_active = [&](int st) -> bool {
-        const int kbase = st * SK;
+        const int kbase = k0 + st * SK;
         if (kbase >= seq_k) return false;
         if (VARIANT != 1 && causal && kbase > row_first + 15) return false;
         return true;
@@ -425,16 +452,18 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         // is issued right after stage st's softmax + PV, and one barrier
         // closes the step.  The loop is unrolled by two so every buffer is a
         // compile-time choice.
-        fill_stage(KL, Kh, 0, Kb0);
-        if (nst > 1) fill_stage(KL, Kh, SK, Kb1);
-        fill_stage(VL, Vh, 0, Vb0);
+        if (nst > 0) {
+            fill_stage(KL, Kh, k0, Kb0);
+            fill_stage(VL, Vh, k0, Vb0);
+        }
+        if (nst > 1) fill_stage(KL, Kh, k0 + SK, Kb1);
         wait_vmcnt<0>();
         __syncthreads();
         f32x4 s_cur[KB];
         bool act_cur = nst > 0 && stage_active(0);
         if (act_cur) {
             qk_stage(Kb0, s_cur);
-            mask_stage(s_cur, 0);
+            mask_stage(s_cur, k0);
         }
         __syncthreads();   // Kb0 free for K(2)
         auto step = [&](auto parity, int st) {
@@ -444,8 +473,8 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             const float* k_next = P ? Kb0 : Kb1;  // K(st+1)
             const float* v_cur = P ? Vb1 : Vb0;   // V(st)
             const bool has_next = st + 1 < nst;
-            if (st + 2 < nst) fill_stage(KL, Kh, (st + 2) * SK, k_fill);
-            if (has_next) fill_stage(VL, Vh, (st + 1) * SK, v_fill);
+            if (st + 2 < nst) fill_stage(KL, Kh, k0 + (st + 2) * SK, k_fill);
+            if (has_next) fill_stage(VL, Vh, k0 + (st + 1) * SK, v_fill);
             const bool act_nxt = has_next && stage_active(st + 1);
             // This stage's softmax + PV, then the next stage's QK^T from the
             // other buffer, with no barrier between them: the second wave on
@@ -453,7 +482,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             if (act_cur) softmax_pv(s_cur, v_cur);
             if (act_nxt) {
                 qk_stage(k_next, s_cur);
-                mask_stage(s_cur, (st + 1) * SK);
+                mask_stage(s_cur, k0 + (st + 1) * SK);
             }
             wait_vmcnt<0>();
             __syncthreads();
@@ -468,25 +497,49 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         // registers before the current stage computes.
         f32x4 kr[LOAD_ITERS], vr[LOAD_ITERS];
         if (nst > 0) {
-            load_regs(Kh, 0, kr);
-            load_regs(Vh, 0, vr);
+            load_regs(Kh, k0, kr);
+            load_regs(Vh, k0, vr);
         }
         for (int st = 0; st < nst; ++st) {
             store_regs(KL, Kb0, kr);
             store_regs(VL, Vb0, vr);
             __syncthreads();
             if (st + 1 < nst) {
-                load_regs(Kh, (st + 1) * SK, kr);
-                load_regs(Vh, (st + 1) * SK, vr);
+                load_regs(Kh, k0 + (st + 1) * SK, kr);
+                load_regs(Vh, k0 + (st + 1) * SK, vr);
             }
             if (stage_active(st)) {
                 f32x4 s[KB];
                 qk_stage(Kb0, s);
-                mask_stage(s, st * SK);
+                mask_stage(s, k0 + st * SK);
                 softmax_pv(s, Vb0);
             }
             __syncthreads();
         }
+    }
+
+    if (splitk) {
+        // Partial for this wave's 16-row tile and this key split, in the
+        // split-KV layout fa_merge reads: O rows (unnormalised), m, l.
+        const int qt = q0 / 16 + wave;
+        if (qt >= p.nqt) return;
+        const float lt = row4_sum(l);
+        const size_t pidx = ((size_t)bh * p.nqt + qt) * p.num_splits + ysplit;
+        float* po = p.part_o + pidx * 16 * D;
+        float* pml = p.part_ml + pidx * 32;
+        if (g == 0) {
+            pml[li] = m;
+            pml[16 + li] = lt;
+        }
+#pragma unroll
+        for (int hh = 0; hh < NVR; ++hh)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int dv0 = 64 * hh + VW * (4 * g + r);
+#pragma unroll
+                for (int j = 0; j < VW; ++j) po[li * D + dv0 + j] = o[VW * hh + j][r];
+            }
+        return;
     }
 
     // Final normalisation with the l > 0 guard (src/v2.rs:375-382; v1's
@@ -770,9 +823,15 @@ __device__ __forceinline__ void merge_body(const FaParams& p) {
     const int row = blockIdx.x;              // bh * seq_q + q
     const int q = row % p.seq_q, bh = row / p.seq_q;
     const int qt = q / 16, qi = q % 16;
-    const int ns = p.num_splits;
     const float c = p.scale_log2e;
-    const size_t pbase = ((size_t)bh * p.nqt + qt) * ns;
+    const size_t pbase = ((size_t)bh * p.nqt + qt) * p.num_splits;
+    // Splits holding data for this row: all of them for split-KV; for the
+    // prefill key split, those starting below the row's block key end.
+    int ns = p.num_splits;
+    if (p.ks_rows > 0) {
+        const int kend = p.causal ? min(p.seq_k, (q / p.ks_rows + 1) * p.ks_rows) : p.seq_k;
+        ns = min(ns, (kend + p.split_len - 1) / p.split_len);
+    }
 
     float M = FA_NEG_INF;
     for (int sp = lane; sp < ns; sp += 64) M = fmaxf(M, p.part_ml[(pbase + sp) * 32 + qi]);

@@ -22,8 +22,9 @@ typedef struct FaParams {
     float scale_log2e;   // (1/sqrt(d) computed in f32) * log2(e)
     int nqb;             // prefill: query blocks of 128 rows
     int nqt;             // split-KV: query tiles of 16 rows
-    int num_splits;      // split-KV: key splits per (bh, query tile)
-    int split_len;       // split-KV: keys per split (multiple of 64)
+    int num_splits;      // split-KV / key split: key splits per (bh, query tile)
+    int split_len;       // keys per split (split-KV: multiple of 64; key split: of the stage)
+    int ks_rows;         // key split: query rows per prefill block (0: split-KV decode)
 } FaParams;
 
 
@@ -36,7 +37,11 @@ typedef struct FaParams {
 #ifdef __cplusplus
 constexpr int fa_prefill_waves(int D) { return D <= 128 ? FA_PREFILL_WAVES : 8; }
 constexpr int fa_prefill_rows(int D) { return 16 * fa_prefill_waves(D); }
-constexpr int fa_prefill_stage_keys(int D) { return D <= 128 ? (fa_prefill_waves(D) == 8 ? 64 : 32) : 32; }
+// d = 256: v3 keeps two stages resident and fits its registers only with
+// 16-key stages; v1/v2 (one stage) use 32.
+constexpr int fa_prefill_stage_keys(int D, int variant) {
+    return D <= 128 ? (fa_prefill_waves(D) == 8 ? 64 : 32) : (variant == 3 ? 16 : 32);
+}
 #endif
 
 #endif

@@ -133,8 +133,10 @@ int fa_device_v3(void* stream, const float* q, const float* k, const float* v, s
 /* ---- extension: explicit scale and path control ------------------------
  * Not in the reference.  softmax_scale <= 0 or NaN keeps the reference's
  * 1/sqrt(d_head).  path: FA_PATH_AUTO (what fa_device_vN does),
- * FA_PATH_PREFILL (never split keys), FA_PATH_SPLITKV (always split; v2/v3
- * only).  num_splits = 0 lets the library choose. */
+ * FA_PATH_PREFILL (query-block kernel; with num_splits > 1 and v2/v3, each
+ * block's keys are divided over num_splits workgroups whose partials are
+ * merged), FA_PATH_SPLITKV (16-row decode tiles, always split; v2/v3 only).
+ * num_splits = 0 lets the library choose (at most 1024). */
 #define FA_PATH_AUTO 0
 #define FA_PATH_PREFILL 1
 #define FA_PATH_SPLITKV 2

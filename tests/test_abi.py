@@ -182,6 +182,22 @@ def test_planning_split_kv():
     assert s.startswith("fa_decode_d64_1 grid=3x3x1") and "splits=3 split_len=128" in s
 
 
+def test_planning_key_split_prefill():
+    # config 5c: 8 query blocks x 16 heads = 128 workgroups < 256 CUs
+    s = describe(3, 1, 16, 1000, 1000, 256, True)
+    assert s.startswith("fa_prefill_v3_d256_2 grid=") and "fa_merge_d256 grid=16000x1x1" in s
+    nks, split_len = int(s.split("splits=")[1].split()[0]), int(s.split("split_len=")[1])
+    assert split_len % 16 == 0 and nks * split_len >= 1000 > (nks - 1) * split_len
+    # compact grid: split y of every 128-row block whose causal key end passes y * split_len
+    wgs = 16 * sum(1 for y in range(nks) for qb in range(8) if min(1000, 128 * (qb + 1)) > y * split_len)
+    assert f"grid={wgs}x1x1" in s
+    assert "fa_merge" not in describe(1, 1, 16, 1000, 1000, 256, True)     # v1 never splits
+    assert "fa_merge" not in describe(3, 1, 32, 2048, 2048, 128, True)    # full grid
+    s = describe(2, 1, 1, 300, 700, 64, False, fa.PATH_PREFILL, 3)   # 11 stages of 64 keys -> 4 per split
+    assert s.startswith("fa_prefill_v2_d64_1 grid=9x1x1") and "splits=3 split_len=256" in s
+    assert "splits=6 split_len=128" in describe(3, 1, 1, 300, 700, 64, False, fa.PATH_PREFILL, 6)
+
+
 def test_planning_errors():
     with pytest.raises(fa.FaError) as e:
         describe(2, 1, 1, 10, 10, 257, False)

@@ -318,6 +318,32 @@ def test_split_kv_matches_oracle_and_prefill():
                 assert_parity(got, want, f"split-kv v{variant} splits={splits} {bh},{sq},{sk},{d},{causal}")
 
 
+def test_key_split_prefill_matches_oracle():
+    """v2/v3 query-block kernel with each block's keys divided over several
+    workgroups and the partials merged (forced here; chosen automatically on
+    grids smaller than the GPU)."""
+    rng = np.random.default_rng(78)
+    cases = [(1, 1000, 1000, 256, True), (2, 300, 700, 64, False), (1, 700, 300, 128, True),
+             (3, 129, 1025, 32, True), (1, 257, 513, 17, False), (2, 200, 2000, 128, False)]
+    for bh, sq, sk, d, causal in cases:
+        q = rng.standard_normal(bh * sq * d, dtype=np.float32)
+        k = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        v = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+        for splits in (2, 3, 5, 16):
+            for variant in (2, 3):
+                tag = f"key-split v{variant} splits={splits} {bh},{sq},{sk},{d},{causal}"
+                print("[case]", tag, flush=True)
+                got = _device_run(variant, q, k, v, bh, sq, sk, d, causal, fa.PATH_PREFILL, splits, guard=64)
+                assert_parity(got, want, tag)
+        # automatic choice (small grid) and its determinism
+        for variant in (2, 3):
+            a = _device_run(variant, q, k, v, bh, sq, sk, d, causal, guard=64)
+            b = _device_run(variant, q, k, v, bh, sq, sk, d, causal, guard=64)
+            assert np.array_equal(a, b)
+            assert_parity(a, want, f"auto v{variant} {bh},{sq},{sk},{d},{causal}")
+
+
 def test_device_api_bounds_and_determinism():
     for bh, sq, sk, d, causal in [(3, 130, 77, 128, True), (2, 257, 300, 64, False), (1, 129, 129, 256, True),
                                   (2, 100, 50, 20, False), (5, 3, 1000, 128, False)]:
