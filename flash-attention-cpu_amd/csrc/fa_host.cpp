@@ -362,12 +362,11 @@ int check_single(size_t q_len, size_t k_len, size_t v_len, size_t out_len, size_
     return FA_OK;
 }
 
-// Host slices: copy in, run, copy out, synchronise.  Serialised per device.
-int run_host(int variant, const float* q, const float* k, const float* v, size_t bh, size_t sq, size_t sk,
-             size_t d, const fa_config* cfg, float* out) {
-    if (bh == 0 || sq == 0 || sk == 0 || d == 0) return FA_OK;   // out untouched
-    if (!q || !k || !v || !out) return FA_ERR_INVALID_ARG;
-    const int causal = cfg ? cfg->causal : 0;
+// Host slices: copy in, run `run(stream, dq, dk, dv, dout)` on the device
+// copies, copy out, synchronise.  Serialised per device.
+template <typename F>
+int with_host_slices(const float* q, const float* k, const float* v, size_t bh, size_t sq, size_t sk, size_t d,
+                     float* out, F&& run) {
     int dev;
     int rc = current_device(&dev);
     if (rc != FA_OK) return rc;
@@ -402,13 +401,13 @@ int run_host(int variant, const float* q, const float* k, const float* v, size_t
     float* dout = dv + up(nk);
     hipStream_t st = s.io_stream;
     if (hipMemcpyAsync(dq, q, nq * sizeof(float), hipMemcpyHostToDevice, st) != hipSuccess ||
-        hipMemcpyAsync(dk, k, nk * sizeof(float), hipMemcpyHostToDevice, st) != hipSuccess ||
-        hipMemcpyAsync(dv, v, nk * sizeof(float), hipMemcpyHostToDevice, st) != hipSuccess) {
+        (nk > 0 && hipMemcpyAsync(dk, k, nk * sizeof(float), hipMemcpyHostToDevice, st) != hipSuccess) ||
+        (nk > 0 && hipMemcpyAsync(dv, v, nk * sizeof(float), hipMemcpyHostToDevice, st) != hipSuccess)) {
         (void)hipGetLastError();
         (void)hipStreamSynchronize(st);
         return FA_ERR_COPY;
     }
-    rc = run_device(variant, st, dq, dk, dv, bh, sq, sk, d, causal, nullptr, dout);
+    rc = run(st, dq, dk, dv, dout);
     if (rc != FA_OK) {
         (void)hipStreamSynchronize(st);
         return rc;
@@ -419,6 +418,100 @@ int run_host(int variant, const float* q, const float* k, const float* v, size_t
         return FA_ERR_COPY;
     }
     return FA_OK;
+}
+
+int run_host(int variant, const float* q, const float* k, const float* v, size_t bh, size_t sq, size_t sk,
+             size_t d, const fa_config* cfg, float* out) {
+    if (bh == 0 || sq == 0 || sk == 0 || d == 0) return FA_OK;   // out untouched
+    if (!q || !k || !v || !out) return FA_ERR_INVALID_ARG;
+    const int causal = cfg ? cfg->causal : 0;
+    return with_host_slices(q, k, v, bh, sq, sk, d, out,
+                            [&](hipStream_t st, const float* dq, const float* dk, const float* dv, float* dout) {
+                                return run_device(variant, st, dq, dk, dv, bh, sq, sk, d, causal, nullptr, dout);
+                            });
+}
+
+// ---------------------------------------------------------------------------
+// Naive attention (src/naive.rs:14-75) on device pointers: scores, row
+// softmax and PV kernels over a materialised [heads, seq_q, seq_k] buffer,
+// heads taken in chunks whose buffer stays within kNaiveChunkBytes.
+// ---------------------------------------------------------------------------
+constexpr size_t kNaiveChunkBytes = size_t(8) << 30;
+
+int launch_naive(int dev, const char* name, unsigned gx, unsigned gy, unsigned gz, NaiveParams* p,
+                 hipStream_t stream) {
+    hipFunction_t fn;
+    int rc = get_function(dev, name, &fn);
+    if (rc != FA_OK) return rc;
+    void* args[] = {p};
+    if (hipModuleLaunchKernel(fn, gx, gy, gz, 256, 1, 1, 0, stream, args, nullptr) != hipSuccess) {
+        (void)hipGetLastError();
+        return FA_ERR_LAUNCH;
+    }
+    return FA_OK;
+}
+
+int run_naive_device(hipStream_t stream, const float* q, const float* k, const float* v, size_t bh, size_t sq,
+                     size_t sk, size_t d, int causal, int precision, float* out) {
+    // The crate writes out = 0 when seq_len_k == 0 (every row's fill(0.0),
+    // src/naive.rs:64); nothing is written when seq_len_q or d_head is 0.
+    if (bh == 0 || sq == 0 || d == 0) return FA_OK;
+    if (!q || !out || (sk > 0 && (!k || !v))) return FA_ERR_INVALID_ARG;
+    if (precision != FA_NAIVE_F32 && precision != FA_NAIVE_F64) return FA_ERR_INVALID_ARG;
+    const size_t imax = 0x7fffffff;
+    if (sq > imax || sk > imax || d > imax || (sq + 63) / 64 > 65535 || (d + 63) / 64 > 65535)
+        return FA_ERR_UNSUPPORTED;
+    int dev;
+    int rc = current_device(&dev);
+    if (rc != FA_OK) return rc;
+    rc = ensure_loaded(dev);
+    if (rc != FA_OK) return rc;
+
+    const bool f64 = precision == FA_NAIVE_F64;
+    const size_t head_bytes = sq * sk * (f64 ? 8 : 4);
+    size_t chunk = head_bytes ? std::max<size_t>(1, kNaiveChunkBytes / head_bytes) : bh;
+    chunk = std::min({chunk, bh, (size_t)65535, imax / sq});
+    void* s = nullptr;
+    if (head_bytes) {
+        if (hipMallocAsync(&s, chunk * head_bytes, stream) != hipSuccess) {
+            (void)hipGetLastError();
+            return FA_ERR_ALLOC;
+        }
+    }
+    const char* sfx = f64 ? "f64" : "f32";
+    std::string n_scores = std::string("fa_naive_scores_") + sfx, n_softmax = std::string("fa_naive_softmax_") + sfx,
+                n_pv = std::string("fa_naive_pv_") + sfx;
+    for (size_t h0 = 0; h0 < bh && rc == FA_OK; h0 += chunk) {
+        const size_t nh = std::min(chunk, bh - h0);
+        NaiveParams p;
+        std::memset(&p, 0, sizeof(p));
+        p.q = q + h0 * sq * d;
+        p.k = sk ? k + h0 * sk * d : nullptr;
+        p.v = sk ? v + h0 * sk * d : nullptr;
+        p.out = out + h0 * sq * d;
+        p.s = s;
+        p.seq_q = static_cast<int>(sq);
+        p.seq_k = static_cast<int>(sk);
+        p.d = static_cast<int>(d);
+        p.causal = causal ? 1 : 0;
+        p.scale_f = 1.0f / std::sqrt(static_cast<float>(d));   // src/naive.rs:29
+        p.scale_d = 1.0 / std::sqrt(static_cast<double>(d));
+        const unsigned gq = static_cast<unsigned>((sq + 63) / 64);
+        if (sk > 0) {
+            rc = launch_naive(dev, n_scores.c_str(), static_cast<unsigned>((sk + 63) / 64), gq,
+                              static_cast<unsigned>(nh), &p, stream);
+            if (rc == FA_OK)
+                rc = launch_naive(dev, n_softmax.c_str(), static_cast<unsigned>(nh * sq), 1, 1, &p, stream);
+        }
+        if (rc == FA_OK)
+            rc = launch_naive(dev, n_pv.c_str(), static_cast<unsigned>((d + 63) / 64), gq, static_cast<unsigned>(nh),
+                              &p, stream);
+    }
+    if (s && hipFreeAsync(s, stream) != hipSuccess) {
+        (void)hipGetLastError();
+        if (rc == FA_OK) rc = FA_ERR_ALLOC;
+    }
+    return rc;
 }
 
 int single(int variant, const float* q, size_t q_len, const float* k, size_t k_len, const float* v,
@@ -532,6 +625,25 @@ int fa_device_v3(void* stream, const float* q, const float* k, const float* v, s
                  size_t sq, size_t sk, size_t d, const fa_config* cfg, float* out) {
     return run_device(3, static_cast<hipStream_t>(stream), q, k, v, batch * heads, sq, sk, d,
                       cfg ? cfg->causal : 0, nullptr, out);
+}
+
+int fa_naive_attention(const float* q, size_t q_len, const float* k, size_t k_len, const float* v, size_t v_len,
+                       size_t sq, size_t sk, size_t d, int causal, float* out, size_t out_len) {
+    // assert_eq! order of src/naive.rs:24-27
+    int rc = check_single(q_len, k_len, v_len, out_len, sq, sk, d);
+    if (rc != FA_OK) return rc;
+    if (sq == 0 || d == 0) return FA_OK;
+    if (!q || !out || (sk > 0 && (!k || !v))) return FA_ERR_INVALID_ARG;
+    return with_host_slices(q, k, v, 1, sq, sk, d, out,
+                            [&](hipStream_t st, const float* dq, const float* dk, const float* dv, float* dout) {
+                                return run_naive_device(st, dq, dk, dv, 1, sq, sk, d, causal, FA_NAIVE_F32, dout);
+                            });
+}
+
+int fa_naive_device(void* stream, const float* q, const float* k, const float* v, size_t batch, size_t heads,
+                    size_t sq, size_t sk, size_t d, int causal, int precision, float* out) {
+    return run_naive_device(static_cast<hipStream_t>(stream), q, k, v, batch * heads, sq, sk, d, causal, precision,
+                            out);
 }
 
 int fa_device_ex(int variant, void* stream, const float* q, const float* k, const float* v, size_t batch,

@@ -2,33 +2,32 @@
 //
 // Replaces the reference crate's per-variant tiling loops and Kernel-trait
 // micro-kernels (amaye15/flash-attention-cpu):
-//   run_v1  src/v1.rs:162-396   -> fa_prefill<.., VARIANT=1, ..>
-//   run_v2  src/v2.rs:160-385   -> fa_prefill<.., VARIANT=2, ..>
-//   run_v3  src/v3.rs:351-512   -> fa_prefill<.., VARIANT=3, ..>
-//   dot4x4 / dot4 / dot         -> QK^T on v_mfma_f32_32x32x2_f32
-//   max_reduce4 / sub_exp_sum4  -> per-lane max/exp2/sum + v_permlane32_swap
-//   pv4 / axpy / scale_inplace  -> PV on v_mfma_f32_32x32x2_f32, per-lane rescale
-//   (new) split-KV + LSE merge  -> fa_decode / fa_merge for short-query shapes
+//   run_v1  src/v1.rs:162-396   -> prefill_body<D, 1, LOADER>
+//   run_v2  src/v2.rs:160-385   -> prefill_body<D, 2, LOADER>
+//   run_v3  src/v3.rs:351-512   -> prefill_body<D, 3, LOADER>
+//   dot4x4 / dot4 / dot         -> QK^T on v_mfma_f32_16x16x4_f32
+//   max_reduce4 / sub_exp_sum4  -> per-lane max/exp2/sum + permlane swaps
+//   pv4 / axpy / scale_inplace  -> PV on v_mfma_f32_16x16x4_f32, per-lane rescale
+//   naive_attention src/naive.rs:14-75 -> naive_{scores,softmax,pv}_body
+//   (new) split-KV + LSE merge  -> decode_body / merge_body (short queries,
+//                                  and the prefill key split on small grids)
 //
-// All arithmetic is IEEE f32 (f32 MFMA, no reduced-precision inputs).
+// All arithmetic is IEEE f32 (f32 MFMA, no reduced-precision inputs); the
+// naive kernels also have an f64 instantiation for on-device checking.
 //
-// Prefill geometry (D = d_head padded to 32/64/128/256):
-//   * one workgroup owns BQ = 128 query rows of one (batch*head) slice;
-//     wave w owns rows 32*(w%4) .. +32 of that block;
-//   * keys are processed in wave tiles of 32; with KSPLIT = 2 (D <= 128) a
-//     workgroup has 8 waves and wave w takes the tiles of parity w/4, so every
-//     SIMD runs two waves on the same rows (one hides the other's softmax);
-//     the two partial (m, l, O) are merged through LDS at the end;
-//   * a stage of KSPLIT*32 keys of K and V sits in LDS, rows padded to D+4
-//     floats (conflict-free 128-bit reads);
-//   * scores are computed transposed, S^T = K Q^T (A = K rows from LDS, B = Q
-//     held in VGPRs), so each lane owns one query row and 16 of the tile's
-//     keys; its partner lane (lane ^ 32) owns the other 16;
+// Prefill geometry (D = d_head padded to 32/64/128/256; fa_params.h):
+//   * a workgroup of NW = 8 waves owns BQ = 128 query rows of one
+//     (batch*head) slice; wave w owns rows 16w .. 16w+15;
+//   * keys stream through LDS in stages of SK keys (64 for D <= 128, 32 or
+//     16 for D = 256), K rows padded to D+8 floats and V rows to D+16 (D+8
+//     at D = 32) so 128-bit reads are free of bank conflicts on the 128-bank
+//     LDS; v3 double-buffers K and V and fills them by global->LDS DMA;
+//   * scores are computed transposed, S^T = K Q^T (A = 16 K rows from LDS,
+//     B = the wave's 16 Q rows held in VGPRs), so lane l owns query row l%16
+//     and keys 4(l/16)+r of every 16-key block;
 //   * the exp'd scores are then already the B operand of O^T = V^T P^T, and
 //     each lane's O^T accumulators belong to its own query row, so the
-//     online-softmax rescale is a per-lane multiply;
-//   * V is read with one 128-bit LDS read per MFMA step: lane i of a half
-//     reads V[key][NB*i .. NB*i+NB-1]; accumulator block j holds dv = NB*i+j.
+//     online-softmax rescale is a per-lane multiply.
 //
 // MFMA operand layouts (verified on MI355X):
 //   32x32x2 f32: A[i][k] in lane (i + 32k), B[k][j] in lane (j + 32k),
@@ -872,6 +871,174 @@ __device__ __forceinline__ void merge_body(const FaParams& p) {
 }
 
 // ---------------------------------------------------------------------------
+// Naive attention: the textbook three passes over a materialised score
+// matrix (src/naive.rs:14-75), kept as an on-device reference -- in f32 as
+// the crate computes it, or in f64 to check the fast kernels on shapes too
+// large for a CPU oracle.  Scores and probabilities live in one
+// [heads, seq_q, seq_k] buffer of T.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ T naive_scale(const NaiveParams& p);
+template <>
+__device__ __forceinline__ float naive_scale<float>(const NaiveParams& p) { return p.scale_f; }
+template <>
+__device__ __forceinline__ double naive_scale<double>(const NaiveParams& p) { return p.scale_d; }
+
+__device__ __forceinline__ float naive_exp(float x) { return expf(x); }
+__device__ __forceinline__ double naive_exp(double x) { return exp(x); }
+
+// S[i][j] = (q_i . k_j) * scale, -inf where causal && j > i
+// (src/naive.rs:33-44).  64x64 tile per 256-thread workgroup, 4x4 per
+// thread (rows ty + 16x, columns tx + 16y), d in chunks of 16 through LDS.
+template <typename T>
+__device__ __forceinline__ void naive_scores_body(const NaiveParams& p) {
+    constexpr int TM = 64, TK = 16;
+    __shared__ T Qs[TK][TM + 1];
+    __shared__ T Ks[TK][TM + 1];
+    const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+    const int j0 = blockIdx.x * TM, i0 = blockIdx.y * TM, h = blockIdx.z;
+    const int sq = p.seq_q, sk = p.seq_k, d = p.d;
+    const float* __restrict__ Q = p.q + (size_t)h * sq * d;
+    const float* __restrict__ K = p.k + (size_t)h * sk * d;
+    T* __restrict__ S = static_cast<T*>(p.s) + (size_t)h * sq * sk;
+    T acc[4][4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int y = 0; y < 4; ++y) acc[x][y] = T(0);
+    const bool all_future = p.causal && j0 > i0 + TM - 1;   // every score of the tile is masked
+    if (!all_future) {
+        for (int kc = 0; kc < d; kc += TK) {
+            for (int e = threadIdx.x; e < TM * TK; e += 256) {
+                const int r = e / TK, c = e % TK, dc = kc + c;
+                Qs[c][r] = (i0 + r < sq && dc < d) ? T(Q[(size_t)(i0 + r) * d + dc]) : T(0);
+                Ks[c][r] = (j0 + r < sk && dc < d) ? T(K[(size_t)(j0 + r) * d + dc]) : T(0);
+            }
+            __syncthreads();
+#pragma unroll
+            for (int c = 0; c < TK; ++c) {
+                T a[4], b[4];
+#pragma unroll
+                for (int x = 0; x < 4; ++x) {
+                    a[x] = Qs[c][ty + 16 * x];
+                    b[x] = Ks[c][tx + 16 * x];
+                }
+#pragma unroll
+                for (int x = 0; x < 4; ++x)
+#pragma unroll
+                    for (int y = 0; y < 4; ++y) acc[x][y] = fma(a[x], b[y], acc[x][y]);
+            }
+            __syncthreads();
+        }
+    }
+    const T scale = naive_scale<T>(p);
+    const T ninf = -__builtin_huge_val();
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+        const int i = i0 + ty + 16 * x;
+        if (i >= sq) continue;
+#pragma unroll
+        for (int y = 0; y < 4; ++y) {
+            const int j = j0 + tx + 16 * y;
+            if (j < sk) S[(size_t)i * sk + j] = (p.causal && j > i) ? ninf : acc[x][y] * scale;
+        }
+    }
+}
+
+// Row softmax in place (src/naive.rs:46-59): max, exp(s - max) and its sum,
+// then multiply by (sum > 0 ? 1/sum : 0).  One 256-thread workgroup per row.
+template <typename T>
+__device__ __forceinline__ T naive_block_reduce(T v, bool is_max, T* red) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const T o = __shfl_xor(v, off);
+        v = is_max ? (o > v ? o : v) : v + o;
+    }
+    const int wave = threadIdx.x / 64;
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    T r = red[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) r = is_max ? (red[w] > r ? red[w] : r) : r + red[w];
+    __syncthreads();
+    return r;
+}
+
+template <typename T>
+__device__ __forceinline__ void naive_softmax_body(const NaiveParams& p) {
+    __shared__ T red[4];
+    const int sk = p.seq_k;
+    T* __restrict__ s = static_cast<T*>(p.s) + (size_t)blockIdx.x * sk;   // row (head, i) of this chunk
+    T m = -__builtin_huge_val();
+    for (int j = threadIdx.x; j < sk; j += 256) m = s[j] > m ? s[j] : m;
+    m = naive_block_reduce<T>(m, true, red);
+    T sum = T(0);
+    for (int j = threadIdx.x; j < sk; j += 256) {
+        const T e = naive_exp(s[j] - m);
+        s[j] = e;
+        sum += e;
+    }
+    sum = naive_block_reduce<T>(sum, false, red);
+    const T inv = sum > T(0) ? T(1) / sum : T(0);
+    for (int j = threadIdx.x; j < sk; j += 256) s[j] *= inv;
+}
+
+// out[i][c] = sum_j P[i][j] V[j][c], skipping p == 0 (src/naive.rs:61-74);
+// with causal masking P is exactly 0 past the tile's last row, so those keys
+// are not visited.  64 rows x 64 columns per workgroup, keys in chunks of 16.
+template <typename T>
+__device__ __forceinline__ void naive_pv_body(const NaiveParams& p) {
+    constexpr int TM = 64, TK = 16;
+    __shared__ T Ps[TK][TM + 1];
+    __shared__ T Vs[TK][TM + 1];
+    const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+    const int c0 = blockIdx.x * TM, i0 = blockIdx.y * TM, h = blockIdx.z;
+    const int sq = p.seq_q, sk = p.seq_k, d = p.d;
+    const T* __restrict__ P = static_cast<const T*>(p.s) + (size_t)h * sq * sk;
+    const float* __restrict__ V = p.v + (size_t)h * sk * d;
+    float* __restrict__ O = p.out + (size_t)h * sq * d;
+    T acc[4][4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int y = 0; y < 4; ++y) acc[x][y] = T(0);
+    const int jend = p.causal ? min(sk, i0 + TM) : sk;
+    for (int jc = 0; jc < jend; jc += TK) {
+        for (int e = threadIdx.x; e < TM * TK; e += 256) {
+            const int r = e / TK, c = e % TK;          // P: row r, key c
+            Ps[c][r] = (i0 + r < sq && jc + c < sk) ? P[(size_t)(i0 + r) * sk + jc + c] : T(0);
+            const int kk = e / TM, cc = e % TM;        // V: key kk, column cc
+            Vs[kk][cc] = (jc + kk < sk && c0 + cc < d) ? T(V[(size_t)(jc + kk) * d + c0 + cc]) : T(0);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < TK; ++c) {
+            T a[4], b[4];
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                a[x] = Ps[c][ty + 16 * x];
+                b[x] = Vs[c][tx + 16 * x];
+            }
+#pragma unroll
+            for (int x = 0; x < 4; ++x)
+#pragma unroll
+                for (int y = 0; y < 4; ++y) acc[x][y] = a[x] != T(0) ? fma(a[x], b[y], acc[x][y]) : acc[x][y];
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+        const int i = i0 + ty + 16 * x;
+        if (i >= sq) continue;
+#pragma unroll
+        for (int y = 0; y < 4; ++y) {
+            const int c = c0 + tx + 16 * y;
+            if (c < d) O[(size_t)i * d + c] = static_cast<float>(acc[x][y]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Named entry points for hipModuleGetFunction.
 // ---------------------------------------------------------------------------
 // fa_prefill_v{V}_d{D}_{L}: L = 0 scalar loads, 1 vector loads, 2 LDS DMA (v3).
@@ -919,3 +1086,14 @@ FA_MERGE(32)
 FA_MERGE(64)
 FA_MERGE(128)
 FA_MERGE(256)
+
+#define FA_NAIVE(T, SUF)                                                                          \
+    extern "C" __global__ void __launch_bounds__(256) fa_naive_scores_##SUF(NaiveParams p) {       \
+        naive_scores_body<T>(p);                                                                  \
+    }                                                                                             \
+    extern "C" __global__ void __launch_bounds__(256) fa_naive_softmax_##SUF(NaiveParams p) {      \
+        naive_softmax_body<T>(p);                                                                 \
+    }                                                                                             \
+    extern "C" __global__ void __launch_bounds__(256) fa_naive_pv_##SUF(NaiveParams p) { naive_pv_body<T>(p); }
+FA_NAIVE(float, f32)
+FA_NAIVE(double, f64)

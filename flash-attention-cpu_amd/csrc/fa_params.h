@@ -28,6 +28,22 @@ typedef struct FaParams {
 } FaParams;
 
 
+// Naive attention (materialised scores): one chunk of heads per launch.
+typedef struct NaiveParams {
+    const float* q;      // [heads, seq_q, d] (this chunk)
+    const float* k;      // [heads, seq_k, d]
+    const float* v;      // [heads, seq_k, d]
+    float* out;          // [heads, seq_q, d]
+    void* s;             // scores / probabilities [heads, seq_q, seq_k], f32 or f64
+    int seq_q;
+    int seq_k;
+    int d;
+    int causal;
+    float scale_f;       // 1/sqrt(d) in f32 (src/naive.rs:29)
+    double scale_d;      // 1/sqrt(d) in f64 (f64 instantiation)
+} NaiveParams;
+
+
 // Prefill geometry shared by the host planner and the kernels: waves per
 // workgroup (each wave owns 16 query rows) and keys per LDS stage.
 // FA_PREFILL_WAVES selects the workgroup size for d_head <= 128.

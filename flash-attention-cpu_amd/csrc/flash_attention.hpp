@@ -122,6 +122,12 @@ inline void flash_attention_multihead_v3(Slice q, Slice k, Slice v, std::size_t 
                                          const FlashAttentionConfig& config, MutSlice out) {
     detail::multi(fa_multihead_v3, q, k, v, batch, heads, seq_len_q, seq_len_k, d_head, config, out);
 }
+// naive_attention -- src/naive.rs:14 (materialised scores, on the GPU)
+inline void naive_attention(Slice q, Slice k, Slice v, std::size_t seq_len_q, std::size_t seq_len_k,
+                            std::size_t d_head, bool causal, MutSlice out) {
+    detail::check(fa_naive_attention(q.data, q.size, k.data, k.size, v.data, v.size, seq_len_q, seq_len_k, d_head,
+                                     causal ? 1 : 0, out.data, out.size));
+}
 // Aliases -- src/lib.rs:86-87
 inline void flash_attention(Slice q, Slice k, Slice v, std::size_t seq_len_q, std::size_t seq_len_k,
                             std::size_t d_head, const FlashAttentionConfig& config, MutSlice out) {

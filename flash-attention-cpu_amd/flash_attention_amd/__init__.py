@@ -50,12 +50,16 @@ PATH_AUTO = 0
 PATH_PREFILL = 1
 PATH_SPLITKV = 2
 
+NAIVE_F32 = 0
+NAIVE_F64 = 1
+
 # Every symbol include/fa_hip.h declares.
 EXPORTED_SYMBOLS = (
     "fa_status_string", "fa_config_default",
     "fa_v1", "fa_v2", "fa_v3", "fa_attention",
     "fa_multihead_v1", "fa_multihead_v2", "fa_multihead_v3", "fa_attention_multihead",
     "fa_device_v1", "fa_device_v2", "fa_device_v3", "fa_device_ex",
+    "fa_naive_attention", "fa_naive_device",
     "fa_init", "fa_describe_launch",
 )
 
@@ -141,6 +145,11 @@ def lib() -> ctypes.CDLL:
     L.fa_device_ex.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                ctypes.c_void_p, _SZ, _SZ, _SZ, _SZ, _SZ, _CFG, _OPTS, ctypes.c_void_p]
     L.fa_device_ex.restype = ctypes.c_int
+    L.fa_naive_attention.argtypes = [_F, _SZ, _F, _SZ, _F, _SZ, _SZ, _SZ, _SZ, ctypes.c_int, _F, _SZ]
+    L.fa_naive_attention.restype = ctypes.c_int
+    L.fa_naive_device.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, _SZ, _SZ,
+                                  _SZ, _SZ, _SZ, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    L.fa_naive_device.restype = ctypes.c_int
     L.fa_init.restype = ctypes.c_int
     L.fa_describe_launch.argtypes = [ctypes.c_int, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_int, _OPTS,
                                      ctypes.c_char_p, _SZ]
@@ -240,6 +249,24 @@ flash_attention_multihead = flash_attention_multihead_v2
 VARIANTS = {1: flash_attention_v1, 2: flash_attention_v2, 3: flash_attention_v3}
 MULTIHEAD_VARIANTS = {1: flash_attention_multihead_v1, 2: flash_attention_multihead_v2,
                       3: flash_attention_multihead_v3}
+
+
+def naive_attention(q, k, v, seq_len_q, seq_len_k, d_head, causal, out) -> None:
+    """naive_attention (src/naive.rs:14): materialised scores, on the GPU, f32."""
+    q, nq = _in(q)
+    k, nk = _in(k)
+    v, nv = _in(v)
+    out = _out(out)
+    _check(lib().fa_naive_attention(_ptr(q), nq, _ptr(k), nk, _ptr(v), nv, seq_len_q, seq_len_k, d_head,
+                                    1 if causal else 0, _ptr(out), out.size))
+
+
+def naive_device(q_ptr: int, k_ptr: int, v_ptr: int, batch: int, heads: int, seq_len_q: int, seq_len_k: int,
+                 d_head: int, causal: bool, out_ptr: int, stream: int = 0, precision: int = NAIVE_F32) -> None:
+    """Queue naive attention on device pointers (fa_naive_device); NAIVE_F64 computes in f64."""
+    _check(lib().fa_naive_device(ctypes.c_void_p(stream), ctypes.c_void_p(q_ptr), ctypes.c_void_p(k_ptr),
+                                 ctypes.c_void_p(v_ptr), batch, heads, seq_len_q, seq_len_k, d_head,
+                                 1 if causal else 0, int(precision), ctypes.c_void_p(out_ptr)))
 
 
 def attention_device(variant: int, q_ptr: int, k_ptr: int, v_ptr: int, batch: int, heads: int,

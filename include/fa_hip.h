@@ -150,6 +150,27 @@ int fa_device_ex(int variant, void* stream, const float* q, const float* k, cons
                  size_t batch, size_t heads, size_t seq_len_q, size_t seq_len_k, size_t d_head,
                  const fa_config* config, const fa_launch_opts* opts, float* out);
 
+/* ---- naive attention (materialised scores) -------------------------------
+ * naive_attention -- src/naive.rs:14-75: the textbook O(seq_q * seq_k)
+ * memory form (scores, row softmax, PV) that the crate keeps as its
+ * correctness oracle, here on the GPU.  Same shape checks and order
+ * (src/naive.rs:24-27); seq_len_q or d_head == 0 writes nothing, seq_len_k
+ * == 0 writes zeros (the crate's out_row.fill).  f32 arithmetic. */
+int fa_naive_attention(const float* q, size_t q_len, const float* k, size_t k_len, const float* v,
+                       size_t v_len, size_t seq_len_q, size_t seq_len_k, size_t d_head, int causal,
+                       float* out, size_t out_len);
+/* Device-resident, multi-head form of the above ([batch, heads, seq, d],
+ * caller's stream).  precision FA_NAIVE_F64 computes scores, softmax and PV
+ * in f64 (output rounded to f32): an on-device reference for checking the
+ * flash kernels at sizes a CPU oracle cannot reach.  The score buffer is
+ * allocated stream-ordered, at most 8 GiB at a time (heads in chunks).  No
+ * counterpart beyond naive_attention itself in the reference. */
+#define FA_NAIVE_F32 0
+#define FA_NAIVE_F64 1
+int fa_naive_device(void* stream, const float* q, const float* k, const float* v, size_t batch,
+                    size_t heads, size_t seq_len_q, size_t seq_len_k, size_t d_head, int causal,
+                    int precision, float* out);
+
 /* ---- introspection -------------------------------------------------------
  * fa_init loads the code object on the current device (done lazily by every
  * entry point).  fa_describe_launch writes the kernel name(s) and grid the

@@ -139,6 +139,28 @@ def test_no_device_fails_loudly():
     with pytest.raises(fa.FaError) as e:
         fa.attention_device(2, 16, 16, 16, 1, 1, 8, 8, d, False, 16)
     assert e.value.status == fa.FA_ERR_NO_DEVICE
+    with pytest.raises(fa.FaError) as e:
+        fa.naive_attention(np.ones(8 * d, np.float32), np.ones(8 * d, np.float32), np.ones(8 * d, np.float32),
+                           8, 8, d, True, out)
+    assert e.value.status == fa.FA_ERR_NO_DEVICE and np.all(out == 7.0)
+
+
+def test_naive_shape_checks_without_device():
+    d = 4
+    q, k, v, o = (np.ones(n * d, np.float32) for n in (3, 5, 5, 3))
+    bad = np.ones(2, np.float32)
+    for args, status in [((bad, k, v, o), fa.FA_ERR_Q_SHAPE), ((q, bad, v, o), fa.FA_ERR_K_SHAPE),
+                         ((q, k, bad, o), fa.FA_ERR_V_SHAPE), ((q, k, v, bad), fa.FA_ERR_OUT_SHAPE),
+                         ((bad, bad, bad, bad), fa.FA_ERR_Q_SHAPE)]:
+        with pytest.raises(fa.ShapeMismatch) as e:
+            fa.naive_attention(args[0], args[1], args[2], 3, 5, d, False, args[3])
+        assert e.value.status == status
+    # seq_len_q == 0 or d_head == 0: nothing to compute, no device needed
+    fa.naive_attention(np.zeros(0, np.float32), k, v, 0, 5, d, False, np.zeros(0, np.float32))
+    fa.naive_attention(*(np.zeros(0, np.float32),) * 3, 3, 5, 0, False, np.zeros(0, np.float32))
+    with pytest.raises(fa.FaError) as e:   # bad precision is rejected before any device work
+        fa.naive_device(16, 16, 16, 1, 1, 3, 5, d, False, 16, 0, 7)
+    assert e.value.status in (fa.FA_ERR_INVALID_ARG, fa.FA_ERR_NO_DEVICE)
 
 
 def test_bad_code_object_path_fails_with_module_or_no_device():
