@@ -73,10 +73,17 @@ class Workload:
         self.bytes = bytes_of(bh, sq, sk, d)
 
 
-def time_steps(torch, fa, wl: Workload, variant: int, steps: int, warmup: int):
-    """W warm-up calls, then K timed calls between synchronisations.
+RAMP_SECONDS = 0.3   # untimed sustained work before each measurement (clock ramp)
 
-    Returns (wall ms per step, kernel-stream ms per step from HIP events)."""
+
+def time_steps(torch, fa, wl: Workload, variant: int, steps: int, warmup: int):
+    """Clock ramp, W warm-up calls, then K timed calls between synchronisations.
+
+    An MI355X coming out of idle runs its first ~10-20 ms of work at a lower
+    clock (measured: the first calls of a run are 10-15 % slower than the
+    steady state), so every measurement first repeats the same call, untimed,
+    for RAMP_SECONDS.  Returns (wall ms per step, kernel-stream ms per step
+    from HIP events)."""
     stream = torch.cuda.current_stream()
     handle = stream.cuda_stream
 
@@ -84,6 +91,13 @@ def time_steps(torch, fa, wl: Workload, variant: int, steps: int, warmup: int):
         fa.attention_device(variant, wl.q.data_ptr(), wl.k.data_ptr(), wl.v.data_ptr(), 1, wl.bh, wl.sq,
                             wl.sk, wl.d, wl.causal, wl.o.data_ptr(), handle)
 
+    t_ramp = time.perf_counter()
+    while True:
+        for _ in range(8):
+            call()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t_ramp >= RAMP_SECONDS:
+            break
     for _ in range(warmup):
         call()
     torch.cuda.synchronize()
@@ -97,6 +111,22 @@ def time_steps(torch, fa, wl: Workload, variant: int, steps: int, warmup: int):
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     return (t1 - t0) * 1e3 / steps, e0.elapsed_time(e1) / steps
+
+
+def time_host_slice(fa, wl: Workload, variant: int, calls: int) -> float:
+    """The drop-in host-slice call (fa_multihead_vN: copy in, run, copy out),
+    ms per call after one warm-up.  PCIe-inclusive; never the headline."""
+    import numpy as np
+
+    q, k, v = wl.q.cpu().numpy(), wl.k.cpu().numpy(), wl.v.cpu().numpy()
+    out = np.empty(wl.bh * wl.sq * wl.d, dtype=np.float32)
+    cfg = fa.FlashAttentionConfig(causal=wl.causal)
+    f = fa.MULTIHEAD_VARIANTS[variant]
+    f(q, k, v, 1, wl.bh, wl.sq, wl.sk, wl.d, cfg, out)
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        f(q, k, v, 1, wl.bh, wl.sq, wl.sk, wl.d, cfg, out)
+    return (time.perf_counter() - t0) * 1e3 / calls
 
 
 def read_traffic(kernel: str, workload: str):
@@ -198,6 +228,11 @@ def main() -> int:
                                     "pct_fp32_mfma_peak": round(100 * head.flops / (m_k * 1e-3) / 1e12
                                                                 / PEAK_TFLOPS, 1)}
         log(f"[bench] config2 v{var}: {m_k * 1e3:.1f} us, {extra[f'config2_v{var}']['tflops']} TFLOP/s")
+    if not args.only_config2:
+        ms = time_host_slice(fa, head, args.variant, 5)
+        extra[f"config2_host_slice_v{args.variant}"] = {"ms_per_call": round(ms, 3),
+                                                        "tflops_incl_pcie": round(head.flops / (ms * 1e-3) / 1e12, 2)}
+        log(f"[bench] config2 host-slice v{args.variant}: {ms:.2f} ms/call incl. PCIe copies")
 
     # Decode shapes: split-KV + merge, bandwidth-bound.
     k_dec = v_dec = None
@@ -212,6 +247,11 @@ def main() -> int:
                                            "pct_hbm_peak": round(100 * gbs / PEAK_GBS, 1),
                                            "kernels": fa.describe_launch(2, 1, 32, sq, 32768, 128, False)}
         log(f"[bench] config4 seq_q={sq}: {m_k * 1e3:.1f} us, {gbs:.0f} GB/s")
+        if sq == 1:
+            ms = time_host_slice(fa, wl, 2, 2)
+            extra["config4_host_slice_sq1"] = {"ms_per_call": round(ms, 2),
+                                               "gbs_incl_pcie": round(wl.bytes / (ms * 1e-3) / 1e9, 1)}
+            log(f"[bench] config4 seq_q=1 host-slice: {ms:.1f} ms/call incl. PCIe copies")
         del wl
     del k_dec, v_dec
     torch.cuda.empty_cache()
