@@ -313,16 +313,21 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     const std::integral_constant<int, LDV> VL{};
 
     // ---- stage math ---------------------------------------------------------
-    // S^T for the stage's KB key blocks from `Ks`.  Blocked summation over
-    // d: each 128-bit K read feeds a fresh 4-step (16-product) MFMA chain
-    // whose result is then added to the running sum.  One long MFMA chain
-    // rounds like a sequential FMA loop; blocks of 16 bring the error down to
-    // that of the crate's 16-lane AVX-512 dot products (src/avx512.rs:195-234),
-    // which matters for large logits.
+    // S^T for the stage's KB key blocks from `Ks`.  An MFMA chain rounds like
+    // a sequential FMA loop, and f32 VALU work does not overlap f32 MFMA on
+    // gfx950, so the summation order trades accuracy against VALU adds:
+    //  * D <= 128: two chains over alternate 16-column chunks of d (at most
+    //    64 products each), added once per stage;
+    //  * D = 256: each 128-bit K read feeds a fresh 4-step (16-product) chain
+    //    that is added to the running sum -- blocks of 16 bring the error down
+    //    to that of the crate's 16-lane AVX-512 dot products
+    //    (src/avx512.rs:195-234), which config 5's large logits need.
+    constexpr bool BLOCKED_QK = D > 128;
     auto qk_stage = [&](const float* Ks, f32x4* s) {
         // K operands one chunk ahead; a scheduling barrier per chunk keeps
         // the live set to two chunks' reads.
         f32x4 kk[2][KB];
+        f32x4 s2[BLOCKED_QK ? 1 : KB];   // second chain (odd chunks)
 #pragma unroll
         for (int b = 0; b < KB; ++b) kk[0][b] = *reinterpret_cast<const f32x4*>(Ks + lds_off<LDK>(16 * b + li, g));
 #pragma unroll
@@ -335,13 +340,27 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             }
 #pragma unroll
             for (int b = 0; b < KB; ++b) {
-                f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
+                if constexpr (BLOCKED_QK) {
+                    f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    t = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[cc & 1][b][i], qreg[4 * cc + i], t, 0, 0, 0);
-                s[b] = (cc == 0) ? t : s[b] + t;
+                    for (int i = 0; i < 4; ++i)
+                        t = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[cc & 1][b][i], qreg[4 * cc + i], t, 0, 0, 0);
+                    s[b] = (cc == 0) ? t : s[b] + t;
+                } else {
+                    f32x4& acc = (cc & 1) ? s2[b] : s[b];
+                    if (cc < 2) acc = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[cc & 1][b][i], qreg[4 * cc + i], acc, 0, 0, 0);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (!BLOCKED_QK) {
+            if constexpr (NC > 1) {
+#pragma unroll
+                for (int b = 0; b < KB; ++b) s[b] += s2[b];
+            }
         }
     };
 
@@ -391,8 +410,12 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             l = l_new;
         } else {
             l = corr * l + ps;
+            // corr is exactly 1 for a row whose maximum did not move; skip
+            // the rescale when that holds for every row of the wave.
+            if (__builtin_amdgcn_ballot_w64(corr != 1.0f) != 0) {
 #pragma unroll
-            for (int j = 0; j < NOB; ++j) o[j] *= corr;
+                for (int j = 0; j < NOB; ++j) o[j] *= corr;
+            }
         }
         // O^T += V^T P^T: 4 keys per MFMA step (key 16b + 4g + r in lane group
         // g).  V operands one step ahead, a scheduling barrier per step.
