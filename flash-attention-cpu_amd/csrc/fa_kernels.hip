@@ -282,27 +282,67 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     // Rows past seq_k are clamped to a real row (masked to -inf / multiplied
     // by 0 later), columns past d and pad slots to column 0, so every read
     // is in bounds.
-    auto dma_stage = [&](auto ld, const float* __restrict__ src, int kbase, float* dst) {
+    //
+    // A full stage (every row below seq_k) is fetched with buffer loads: a
+    // per-stage buffer resource (base = the stage's first row, in SGPRs) and
+    // per-lane byte offsets that are the same for every stage, computed once
+    // below -- no per-stage VALU address arithmetic.  The last, partial stage
+    // takes the clamped per-lane path.
+    auto dma_geometry = [&](auto ld, int* voff) {
         constexpr int RCH = decltype(ld)::value / 4;   // chunks per padded row
         constexpr int TOTAL = SK * RCH;
         constexpr int RUNS = (TOTAL + 63) / 64;
         constexpr int NI = (RUNS + NW - 1) / NW;
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            const int run = i * NW + wave;
-            if (run < RUNS) {
-                const int pos = run * 64 + lane;
-                const int r = pos / RCH, cidx = pos % RCH;
-                const int key = min(kbase + r, seq_k - 1);
-                const int col = (cidx < CPR && 4 * cidx < d) ? 4 * cidx : 0;
-                if (pos < TOTAL)
-                    __builtin_amdgcn_global_load_lds(src + (size_t)key * d + col, dst + run * 256, 16, 0, 0);
+            const int pos = (i * NW + wave) * 64 + lane;
+            const int r = pos / RCH, cidx = pos % RCH;
+            const int col = (cidx < CPR && 4 * cidx < d) ? 4 * cidx : 0;
+            voff[i] = (pos < TOTAL) ? 4 * (r * d + col) : -1;   // -1: lane past the image
+        }
+    };
+    auto dma_stage = [&](auto ld, const float* __restrict__ src, int kbase, float* dst, const int* voff) {
+        constexpr int RCH = decltype(ld)::value / 4;
+        constexpr int TOTAL = SK * RCH;
+        constexpr int RUNS = (TOTAL + 63) / 64;
+        constexpr int NI = (RUNS + NW - 1) / NW;
+        if (kbase + SK <= seq_k) {
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(src + (size_t)kbase * d), (short)0, SK * d * 4, 0x00020000);
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int run = i * NW + wave;
+                // every wave has run i < RUNS while (i + 1) * NW <= RUNS;
+                // only the image's last run can have lanes past it
+                if (((i + 1) * NW <= RUNS || run < RUNS) && (TOTAL % 64 == 0 || run < RUNS - 1 || voff[i] >= 0))
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        rs, (__attribute__((address_space(3))) void*)(dst + run * 256), 16, voff[i], 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int run = i * NW + wave;
+                if ((i + 1) * NW <= RUNS || run < RUNS) {
+                    const int pos = run * 64 + lane;
+                    const int r = pos / RCH, cidx = pos % RCH;
+                    const int key = min(kbase + r, seq_k - 1);
+                    const int col = (cidx < CPR && 4 * cidx < d) ? 4 * cidx : 0;
+                    if (pos < TOTAL)
+                        __builtin_amdgcn_global_load_lds(src + (size_t)key * d + col, dst + run * 256, 16, 0, 0);
+                }
             }
         }
     };
+    constexpr int NI_K = ((SK * (LDK / 4) + 63) / 64 + NW - 1) / NW;
+    constexpr int NI_V = ((SK * (LDV / 4) + 63) / 64 + NW - 1) / NW;
+    int voff_k[DMA ? NI_K : 1], voff_v[DMA ? NI_V : 1];
+    if constexpr (DMA) {
+        dma_geometry(std::integral_constant<int, LDK>{}, voff_k);
+        dma_geometry(std::integral_constant<int, LDV>{}, voff_v);
+    }
     auto fill_stage = [&](auto ld, const float* __restrict__ src, int kbase, float* dst) {
         if constexpr (DMA) {
-            dma_stage(ld, src, kbase, dst);
+            dma_stage(ld, src, kbase, dst, decltype(ld)::value == LDK ? voff_k : voff_v);
         } else {
             f32x4 rg[LOAD_ITERS];
             load_regs(src, kbase, rg);
