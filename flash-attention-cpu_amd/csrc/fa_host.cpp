@@ -261,6 +261,7 @@ int make_plan(int variant, const float* q, const float* k, const float* v, const
                 p.num_splits = static_cast<int>(nks);
                 p.split_len = static_cast<int>(per * SKs);
                 p.ks_rows = static_cast<int>(rows);
+                p.merge_scale = 1.0f;   // prefill partial maxima are in the log2 domain
                 size_t wgs = 0;   // compact grid: split y of every block that reaches it
                 for (size_t y = 0; y < nks; ++y) wgs += (causal ? nqb - std::min(nqb, y * per * SKs / rows) : nqb) * bh;
                 if (wgs > imax) return FA_ERR_UNSUPPORTED;
@@ -294,6 +295,7 @@ int make_plan(int variant, const float* q, const float* k, const float* v, const
     p.nqt = static_cast<int>(nqt);
     p.num_splits = static_cast<int>(nsplit);
     p.split_len = static_cast<int>(split_len);
+    p.merge_scale = p.scale_log2e;   // decode partial maxima are raw scores
     std::snprintf(buf, sizeof(buf), "fa_decode_d%d_%d", D, vec ? 1 : 0);
     plan->first.name = buf;
     plan->first.gx = static_cast<unsigned>(nsplit);

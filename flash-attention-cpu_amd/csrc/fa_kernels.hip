@@ -48,6 +48,10 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 #define FA_NEG_INF (-__builtin_huge_valf())
 
+// Prefill's lazy running max (log2 units): exponentials are taken against a
+// reference that may trail the true row max by up to this much.
+constexpr float kLazyMax = 8.0f;
+
 // ---------------------------------------------------------------------------
 // Small device helpers
 // ---------------------------------------------------------------------------
@@ -226,7 +230,10 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     const float c = p.scale_log2e;
     const bool causal = p.causal != 0;
 
-    // Q rows of this wave as the B operand: lane holds Q[row][16cc + 4g + i].
+    // Q rows of this wave as the B operand: lane holds Q[row][16cc + 4g + i],
+    // pre-multiplied by scale * log2(e) so scores come out of the MFMA in the
+    // exp2 domain (src/v2.rs:171-173 multiplies after the dot; the product
+    // differs by one f32 rounding per element of Q).
     const int row_first = q0 + 16 * wave;
     const int qrow = row_first + li;
     float qreg[NQ];
@@ -234,13 +241,13 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     for (int cc = 0; cc < NC; ++cc) {
         const f32x4 t = load4<LOADER != 0>(Qh, qrow, seq_q, 16 * cc + 4 * g, d);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) qreg[4 * cc + i] = t[i];
+        for (int i = 0; i < 4; ++i) qreg[4 * cc + i] = t[i] * c;
     }
 
     f32x4 o[NOB];
 #pragma unroll
     for (int j = 0; j < NOB; ++j) o[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-    float m = FA_NEG_INF;   // running max of raw scores q.k (same in the row's 4 lanes)
+    float m = FA_NEG_INF;   // reference max of the row's log2-domain scores (same in its 4 lanes)
     float l = 0.0f;         // v2/v3: this lane's partial row sum; v1: full row sum
 
     // Keys this workgroup visits: v1 visits every key (no causal skip,
@@ -428,19 +435,25 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) mt = fmaxf(mt, s[b][r]);
         mt = row4_max(mt);
-        const float m_new = fmaxf(m, mt);
+        // Lazy reference max: it moves only when the stage max exceeds it by
+        // more than kLazyMax (log2 units), so exponentials stay <= 2^kLazyMax
+        // and rescaling the accumulators is rare; otherwise corr is exactly 1.
+        // The final O / l is the same quotient (each term and l share the
+        // reference), to f32 rounding.
+        const bool grow = mt > m + kLazyMax;   // from m = -inf: any visible key
+        const float m_new = grow ? mt : m;
         const float m_use = (m_new == FA_NEG_INF) ? 0.0f : m_new;
-        // (s - m) is exact-rounded and <= 0, so the row maximum maps to
-        // exp2(0) = 1 exactly whatever the magnitude of the scores.
         float ps = 0.0f;
 #pragma unroll
         for (int b = 0; b < KB; ++b)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                s[b][r] = fa_exp2((s[b][r] - m_use) * c);
+                s[b][r] = fa_exp2(s[b][r] - m_use);
                 ps += s[b][r];
             }
-        const float corr = rescale_factor(m, m_use, c);
+        // m = -inf: nothing accumulated yet (o and l are 0), factor 0
+        const float corr = (m == FA_NEG_INF) ? 0.0f : fa_exp2(m - m_new);
+        const bool rescale = grow && m != FA_NEG_INF;
         m = m_new;
         if (VARIANT == 1) {
             const float l_new = corr * l + row4_sum(ps);
@@ -450,9 +463,10 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             l = l_new;
         } else {
             l = corr * l + ps;
-            // corr is exactly 1 for a row whose maximum did not move; skip
-            // the rescale when that holds for every row of the wave.
-            if (__builtin_amdgcn_ballot_w64(corr != 1.0f) != 0) {
+            // corr is exactly 1 for a row whose reference did not move (and
+            // o is still 0 for a row that had none); skip the rescale when
+            // that holds for every row of the wave.
+            if (__builtin_amdgcn_ballot_w64(rescale) != 0) {
 #pragma unroll
                 for (int j = 0; j < NOB; ++j) o[j] *= corr;
             }
@@ -885,7 +899,7 @@ __device__ __forceinline__ void merge_body(const FaParams& p) {
     const int row = blockIdx.x;              // bh * seq_q + q
     const int q = row % p.seq_q, bh = row / p.seq_q;
     const int qt = q / 16, qi = q % 16;
-    const float c = p.scale_log2e;
+    const float c = p.merge_scale;   // partial maxima -> log2 domain
     const size_t pbase = ((size_t)bh * p.nqt + qt) * p.num_splits;
     // Splits holding data for this row: all of them for split-KV; for the
     // prefill key split, those starting below the row's block key end.

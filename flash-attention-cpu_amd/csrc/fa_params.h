@@ -25,6 +25,8 @@ typedef struct FaParams {
     int num_splits;      // split-KV / key split: key splits per (bh, query tile)
     int split_len;       // keys per split (split-KV: multiple of 64; key split: of the stage)
     int ks_rows;         // key split: query rows per prefill block (0: split-KV decode)
+    float merge_scale;   // fa_merge: factor taking partial maxima to the log2 domain
+                         // (split-KV: scale_log2e; prefill key split: 1, already scaled)
 } FaParams;
 
 
