@@ -370,38 +370,68 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     //    to that of the crate's 16-lane AVX-512 dot products
     //    (src/avx512.rs:195-234), which config 5's large logits need.
     constexpr bool BLOCKED_QK = D > 128;
-    auto qk_stage = [&](const float* Ks, f32x4* s) {
-        // K operands one chunk ahead; a scheduling barrier per chunk keeps
-        // the live set to two chunks' reads.
-        f32x4 kk[2][KB];
+    // Read-ahead: the first PRE d-chunks of the next QK^T and the first PRE
+    // V steps of the next PV are read into registers before the softmax VALU
+    // work (the stage is already resident), so their LDS latency is hidden;
+    // inside QK^T and PV the reads then run PRE chunks / steps ahead through
+    // a ring of PRE + 1 register sets, each read issued after the MFMAs that
+    // last used its slot.  D = 256 has no registers to spare: one ahead.
+    constexpr int PRE = (D <= 128) ? 2 : 0;
+    f32x4 kpre[PRE ? PRE : 1][KB];
+    auto k_chunk = [&](const float* Ks, int cc, f32x4* dst) {
+#pragma unroll
+        for (int b = 0; b < KB; ++b) dst[b] = *reinterpret_cast<const f32x4*>(Ks + lds_off<LDK>(16 * b + li, 4 * cc + g));
+    };
+    auto qk_preload = [&](const float* Ks) {
+        if constexpr (PRE > 0) {
+#pragma unroll
+            for (int cc = 0; cc < PRE && cc < NC; ++cc) k_chunk(Ks, cc, kpre[cc]);
+        }
+    };
+    auto qk_mfma = [&](const f32x4* kk, int cc, f32x4* s, f32x4* s2) {
+#pragma unroll
+        for (int b = 0; b < KB; ++b) {
+            if constexpr (BLOCKED_QK) {
+                f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    t = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[b][i], qreg[4 * cc + i], t, 0, 0, 0);
+                s[b] = (cc == 0) ? t : s[b] + t;
+            } else {
+                f32x4& acc = (cc & 1) ? s2[b] : s[b];
+                if (cc < 2) acc = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[b][i], qreg[4 * cc + i], acc, 0, 0, 0);
+            }
+        }
+    };
+    auto qk_stage = [&](const float* Ks, f32x4* s) {   // after qk_preload(Ks)
         f32x4 s2[BLOCKED_QK ? 1 : KB];   // second chain (odd chunks)
+        if constexpr (PRE > 0) {
+            constexpr int KR = PRE + 1;
+            f32x4 kk[KR][KB];
 #pragma unroll
-        for (int b = 0; b < KB; ++b) kk[0][b] = *reinterpret_cast<const f32x4*>(Ks + lds_off<LDK>(16 * b + li, g));
+            for (int cc = 0; cc < PRE && cc < NC; ++cc)
 #pragma unroll
-        for (int cc = 0; cc < NC; ++cc) {
-            if (cc + 1 < NC) {
+                for (int b = 0; b < KB; ++b) kk[cc][b] = kpre[cc][b];
 #pragma unroll
-                for (int b = 0; b < KB; ++b)
-                    kk[(cc + 1) & 1][b] =
-                        *reinterpret_cast<const f32x4*>(Ks + lds_off<LDK>(16 * b + li, 4 * (cc + 1) + g));
+            for (int cc = 0; cc < NC; ++cc) {
+                qk_mfma(kk[cc % KR], cc, s, s2);
+                if (cc + PRE < NC) k_chunk(Ks, cc + PRE, kk[(cc + PRE) % KR]);
+                __builtin_amdgcn_sched_barrier(0);
             }
+        } else {
+            // K operands one chunk ahead; a scheduling barrier per chunk keeps
+            // the live set to two chunks' reads.
+            f32x4 kk[2][KB];
+            k_chunk(Ks, 0, kk[0]);
 #pragma unroll
-            for (int b = 0; b < KB; ++b) {
-                if constexpr (BLOCKED_QK) {
-                    f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        t = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[cc & 1][b][i], qreg[4 * cc + i], t, 0, 0, 0);
-                    s[b] = (cc == 0) ? t : s[b] + t;
-                } else {
-                    f32x4& acc = (cc & 1) ? s2[b] : s[b];
-                    if (cc < 2) acc = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[cc & 1][b][i], qreg[4 * cc + i], acc, 0, 0, 0);
-                }
+            for (int cc = 0; cc < NC; ++cc) {
+                if (cc + 1 < NC) k_chunk(Ks, cc + 1, kk[(cc + 1) & 1]);
+                qk_mfma(kk[cc & 1], cc, s, s2);
+                __builtin_amdgcn_sched_barrier(0);
             }
-            __builtin_amdgcn_sched_barrier(0);
         }
         if constexpr (!BLOCKED_QK) {
             if constexpr (NC > 1) {
@@ -426,8 +456,30 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         }
     };
 
+    // V operands of PV step `step` (keys 16(step/4) + 4g + step%4).
+    auto read_v = [&](const float* Vs, int step, f32x4* vv) {
+        const int kr = 16 * (step / 4) + 4 * g + (step % 4);
+#pragma unroll
+        for (int hh = 0; hh < NVR; ++hh) {
+            if constexpr (VW == 4) {
+                vv[hh] = *reinterpret_cast<const f32x4*>(Vs + lds_off<LDV>(kr, 16 * hh + li));
+            } else {
+                const f32x2 t = *reinterpret_cast<const f32x2*>(Vs + lds_off<LDV>(kr, li >> 1) + 2 * (li & 1));
+                vv[hh] = (f32x4){t[0], t[1], 0.0f, 0.0f};
+            }
+        }
+    };
+    f32x4 vpre[PRE ? PRE : 1][NVR];
+    auto pv_preload = [&](const float* Vs) {
+        if constexpr (PRE > 0) {
+#pragma unroll
+            for (int st = 0; st < PRE; ++st) read_v(Vs, st, vpre[st]);
+        }
+    };
+
     // Online-softmax update + PV for one stage (src/v2.rs:289-372; v1's
-    // normalise / un-normalise round trip, src/v1.rs:291-385).
+    // normalise / un-normalise round trip, src/v1.rs:291-385).  After
+    // pv_preload(Vs).
     auto softmax_pv = [&](f32x4* s, const float* Vs) {
         float mt = s[0][0];
 #pragma unroll
@@ -472,37 +524,36 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             }
         }
         // O^T += V^T P^T: 4 keys per MFMA step (key 16b + 4g + r in lane group
-        // g).  V operands one step ahead, a scheduling barrier per step.
-        auto read_v = [&](int step, f32x4* vv) {
-            const int kr = 16 * (step / 4) + 4 * g + (step % 4);
-#pragma unroll
-            for (int hh = 0; hh < NVR; ++hh) {
-                if constexpr (VW == 4) {
-                    vv[hh] = *reinterpret_cast<const f32x4*>(Vs + lds_off<LDV>(kr, 16 * hh + li));
-                } else {
-                    const f32x2 t = *reinterpret_cast<const f32x2*>(Vs + lds_off<LDV>(kr, li >> 1) + 2 * (li & 1));
-                    vv[hh] = (f32x4){t[0], t[1], 0.0f, 0.0f};
-                }
-            }
-        };
-        constexpr int VBUF = (NVR > 2) ? 1 : 2;   // d = 256: no read-ahead (registers)
-        f32x4 vv[VBUF][NVR];
-        if (VBUF > 1) {
-            read_v(0, vv[0]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-#pragma unroll
-        for (int step = 0; step < 4 * KB; ++step) {
-            if (VBUF == 1) read_v(step, vv[0]);
-            else if (step + 1 < 4 * KB) read_v(step + 1, vv[(step + 1) % VBUF]);
+        // g), a scheduling barrier per step.
+        auto pv_step = [&](int step, const f32x4* vv) {
             const float pr = s[step / 4][step % 4];
 #pragma unroll
             for (int hh = 0; hh < NVR; ++hh)
 #pragma unroll
                 for (int j = 0; j < VW; ++j)
-                    o[VW * hh + j] =
-                        __builtin_amdgcn_mfma_f32_16x16x4f32(vv[step % VBUF][hh][j], pr, o[VW * hh + j], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
+                    o[VW * hh + j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[hh][j], pr, o[VW * hh + j], 0, 0, 0);
+        };
+        if constexpr (PRE > 0) {
+            constexpr int VR = PRE + 1;
+            f32x4 vv[VR][NVR];
+#pragma unroll
+            for (int st = 0; st < PRE; ++st)
+#pragma unroll
+                for (int hh = 0; hh < NVR; ++hh) vv[st][hh] = vpre[st][hh];
+#pragma unroll
+            for (int step = 0; step < 4 * KB; ++step) {
+                pv_step(step, vv[step % VR]);
+                if (step + PRE < 4 * KB) read_v(Vs, step + PRE, vv[(step + PRE) % VR]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+            f32x4 vv[NVR];   // d = 256: no read-ahead (registers)
+#pragma unroll
+            for (int step = 0; step < 4 * KB; ++step) {
+                read_v(Vs, step, vv);
+                pv_step(step, vv);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
         if (VARIANT == 1) {
             const float inv = l > 0.0f ? 1.0f / l : 0.0f;
@@ -538,6 +589,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         f32x4 s_cur[KB];
         bool act_cur = nst > 0 && stage_active(0);
         if (act_cur) {
+            qk_preload(Kb0);
             qk_stage(Kb0, s_cur);
             mask_stage(s_cur, k0);
         }
@@ -553,8 +605,10 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             if (has_next) fill_stage(VL, Vh, k0 + (st + 1) * SK, v_fill);
             const bool act_nxt = has_next && stage_active(st + 1);
             // This stage's softmax + PV, then the next stage's QK^T from the
-            // other buffer, with no barrier between them: the second wave on
-            // each SIMD runs one while this wave runs the other.
+            // other buffer, with no barrier between them.  Both stages are
+            // resident: their first operands are read before the softmax.
+            if (act_cur) pv_preload(v_cur);
+            if (act_nxt) qk_preload(k_next);
             if (act_cur) softmax_pv(s_cur, v_cur);
             if (act_nxt) {
                 qk_stage(k_next, s_cur);
@@ -586,6 +640,8 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             }
             if (stage_active(st)) {
                 f32x4 s[KB];
+                qk_preload(Kb0);
+                pv_preload(Vb0);
                 qk_stage(Kb0, s);
                 mask_stage(s, k0 + st * SK);
                 softmax_pv(s, Vb0);
