@@ -162,6 +162,15 @@ def cpu_baseline(wl: Workload, budget_s: float):
         if el >= budget_s or n >= 200:
             break
     per_call = el / n
+    model = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
     return {
         "value": round(wl.flops / per_call / 1e12, 4),
         "unit": "TFLOP/s",
@@ -169,7 +178,7 @@ def cpu_baseline(wl: Workload, budget_s: float):
         "kind": "port",
         "sample": (f"{wl.name}: full workload ({wl.bh} heads), {n} calls after 1 warm-up, "
                    f"{per_call * 1e3:.1f} ms/call, oracle v2 {oracle.TIER_NAMES[tier]} tier, "
-                   f"Br=64 Bc=128, {threads} threads"),
+                   f"Br=64 Bc=128, {threads} threads on {model} ({os.cpu_count()} logical CPUs visible)"),
     }
 
 
@@ -218,6 +227,11 @@ def main() -> int:
     log(f"[bench] config2 v{args.variant}: {ms_step * 1e3:.1f} us/step wall, {ms_kernel * 1e3:.1f} us kernel, "
         f"{value:.2f} TFLOP/s")
 
+    if not args.only_config2:
+        # The survey's protocol: R = 5 repeats of 20 launches, median us/call.
+        reps = sorted(time_steps(torch, fa, head, args.variant, 20, 3)[1] for _ in range(5))
+        extra[f"config2_v{args.variant}_median_5x20_us"] = round(reps[2] * 1e3, 1)
+        log(f"[bench] config2 v{args.variant}: median of 5 x 20 launches {reps[2] * 1e3:.1f} us")
     for var in (() if args.only_config2 else (1, 2, 3)):
         if var == args.variant:
             m_w, m_k = ms_step, ms_kernel
