@@ -143,28 +143,31 @@ int pad_d(size_t d) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int make_plan(int variant, const float* q, const float* k, const float* v, const float* out,
+int make_plan(int variant, const void* q, const void* k, const void* v, const float* out,
               size_t bh, size_t sq, size_t sk, size_t d, int causal, const fa_launch_opts* opts,
               int num_cus, Plan* plan) {
     if (variant < 1 || variant > 3) return FA_ERR_INVALID_ARG;
     const int path = opts ? opts->path : FA_PATH_AUTO;
+    const int dtype = opts ? opts->dtype : FA_DTYPE_F32;
+    if (dtype != FA_DTYPE_F32 && dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F16) return FA_ERR_INVALID_ARG;
+    const bool lp = dtype != FA_DTYPE_F32;   // 16-bit inputs: the fa_prefill_lp kernels
     if (path < FA_PATH_AUTO || path > FA_PATH_SPLITKV) return FA_ERR_INVALID_ARG;
-    if (path == FA_PATH_SPLITKV && variant == 1) return FA_ERR_INVALID_ARG;
+    if (path == FA_PATH_SPLITKV && (variant == 1 || lp)) return FA_ERR_INVALID_ARG;
     if (opts && opts->num_splits < 0) return FA_ERR_INVALID_ARG;
     if (d > (size_t)kMaxD) return FA_ERR_UNSUPPORTED;
     const size_t imax = 0x7fffffff;
     if (sq > imax || sk > imax || bh > imax) return FA_ERR_UNSUPPORTED;
 
     const int D = pad_d(d);
-    const bool vec = (d % 4 == 0) && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
+    const bool vec = (d % (lp ? 8 : 4) == 0) && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
     float scale = 1.0f / std::sqrt(static_cast<float>(d));   // src/v2.rs:171
     if (opts && opts->softmax_scale > 0.0f && std::isfinite(opts->softmax_scale)) scale = opts->softmax_scale;
 
     FaParams& p = plan->p;
     std::memset(&p, 0, sizeof(p));
-    p.q = q;
-    p.k = k;
-    p.v = v;
+    p.q = static_cast<const float*>(q);   // 16-bit data for the lp kernels, which reinterpret
+    p.k = static_cast<const float*>(k);
+    p.v = static_cast<const float*>(v);
     p.out = const_cast<float*>(out);
     p.bh = static_cast<int>(bh);
     p.seq_q = static_cast<int>(sq);
@@ -173,11 +176,11 @@ int make_plan(int variant, const float* q, const float* k, const float* v, const
     p.causal = causal ? 1 : 0;
     p.scale_log2e = scale * 1.44269504088896341f;
 
-    const size_t rows = (size_t)fa_prefill_rows(D);   // query rows per prefill workgroup
+    const size_t rows = (size_t)(lp ? fa_lp_rows() : fa_prefill_rows(D));   // query rows per prefill workgroup
     const size_t nqb = (sq + rows - 1) / rows;
     const size_t nqt = (sq + kDecodeRows - 1) / kDecodeRows;
     bool split = false;
-    if (variant != 1) {
+    if (variant != 1 && !lp) {
         if (path == FA_PATH_SPLITKV) {
             split = true;
         } else if (path == FA_PATH_AUTO) {
@@ -193,12 +196,18 @@ int make_plan(int variant, const float* q, const float* k, const float* v, const
     if (!split) {
         if (nqb * bh > imax) return FA_ERR_UNSUPPORTED;
         p.nqb = static_cast<int>(nqb);
-        // 0: scalar loads (any d), 1: 128-bit loads, 2: global->LDS DMA (v3)
-        const int loader = vec ? (variant == 3 ? 2 : 1) : 0;
-        std::snprintf(buf, sizeof(buf), "fa_prefill_v%d_d%d_%d", variant, D, loader);
+        if (lp) {
+            // 0: register-staged scalar loads (any d), 2: global->LDS DMA
+            std::snprintf(buf, sizeof(buf), "fa_prefill_lp_%s_d%d_%d", dtype == FA_DTYPE_BF16 ? "bf16" : "f16", D,
+                          vec ? 2 : 0);
+        } else {
+            // 0: scalar loads (any d), 1: 128-bit loads, 2: global->LDS DMA (v3)
+            const int loader = vec ? (variant == 3 ? 2 : 1) : 0;
+            std::snprintf(buf, sizeof(buf), "fa_prefill_v%d_d%d_%d", variant, D, loader);
+        }
         plan->first.name = buf;
         plan->first.gx = static_cast<unsigned>(nqb * bh);
-        plan->first.bx = 64 * fa_prefill_waves(D);
+        plan->first.bx = lp ? 512 : 64 * fa_prefill_waves(D);
         plan->ws_floats = 0;
         // Key split for v2/v3 when the grid would leave CUs idle: a query
         // block's keys are cut into splits of `per` stages, one workgroup
@@ -211,8 +220,8 @@ int make_plan(int variant, const float* q, const float* k, const float* v, const
         // splits beats several rounds of short ones.  The grid lists only
         // workgroups with keys.
         size_t per = 0;
-        if (variant != 1) {
-            const size_t SKs = (size_t)fa_prefill_stage_keys(D, variant);
+        if (variant != 1 || lp) {
+            const size_t SKs = (size_t)(lp ? fa_lp_stage_keys() : fa_prefill_stage_keys(D, variant));
             auto block_stages = [&](size_t b) {
                 const size_t kend = causal ? std::min(sk, (b + 1) * rows) : sk;
                 return (kend + SKs - 1) / SKs;
@@ -323,7 +332,7 @@ int launch(int dev, const Launch& L, FaParams* p, hipStream_t stream) {
 }
 
 // Queue one attention call on device pointers.
-int run_device(int variant, hipStream_t stream, const float* q, const float* k, const float* v, size_t bh,
+int run_device(int variant, hipStream_t stream, const void* q, const void* k, const void* v, size_t bh,
                size_t sq, size_t sk, size_t d, int causal, const fa_launch_opts* opts, float* out) {
     if (bh == 0 || sq == 0 || sk == 0 || d == 0) return FA_OK;   // src/common.rs:56
     if (!q || !k || !v || !out) return FA_ERR_INVALID_ARG;
@@ -364,11 +373,12 @@ int check_single(size_t q_len, size_t k_len, size_t v_len, size_t out_len, size_
     return FA_OK;
 }
 
-// Host slices: copy in, run `run(stream, dq, dk, dv, dout)` on the device
-// copies, copy out, synchronise.  Serialised per device.
+// Host slices: copy in (Q/K/V elements of `esize` bytes), run
+// `run(stream, dq, dk, dv, dout)` on the device copies, copy the f32 output
+// out, synchronise.  Serialised per device.
 template <typename F>
-int with_host_slices(const float* q, const float* k, const float* v, size_t bh, size_t sq, size_t sk, size_t d,
-                     float* out, F&& run) {
+int with_host_slices(const void* q, const void* k, const void* v, size_t esize, size_t bh, size_t sq, size_t sk,
+                     size_t d, float* out, F&& run) {
     int dev;
     int rc = current_device(&dev);
     if (rc != FA_OK) return rc;
@@ -383,10 +393,11 @@ int with_host_slices(const float* q, const float* k, const float* v, size_t bh, 
             return FA_ERR_LAUNCH;
         }
     }
-    // 64-float alignment keeps every operand 256-byte aligned.
-    auto up = [](size_t n) { return (n + 63) / 64 * 64; };
+    // Regions rounded up to 256 bytes keep every operand 256-byte aligned.
+    auto up = [](size_t bytes) { return (bytes + 255) / 256 * 256; };
     const size_t nq = bh * sq * d, nk = bh * sk * d;
-    const size_t need = up(nq) * 2 + up(nk) * 2;
+    const size_t bq = up(nq * esize), bk = up(nk * esize), bo = up(nq * sizeof(float));
+    const size_t need = (bq + 2 * bk + bo + sizeof(float) - 1) / sizeof(float);
     if (need > s.io_floats) {
         if (s.io_buf) (void)hipFree(s.io_buf);
         s.io_buf = nullptr;
@@ -397,14 +408,15 @@ int with_host_slices(const float* q, const float* k, const float* v, size_t bh, 
         }
         s.io_floats = need;
     }
-    float* dq = s.io_buf;
-    float* dk = dq + up(nq);
-    float* dv = dk + up(nk);
-    float* dout = dv + up(nk);
+    char* base = reinterpret_cast<char*>(s.io_buf);
+    void* dq = base;
+    void* dk = base + bq;
+    void* dv = base + bq + bk;
+    float* dout = reinterpret_cast<float*>(base + bq + 2 * bk);
     hipStream_t st = s.io_stream;
-    if (hipMemcpyAsync(dq, q, nq * sizeof(float), hipMemcpyHostToDevice, st) != hipSuccess ||
-        (nk > 0 && hipMemcpyAsync(dk, k, nk * sizeof(float), hipMemcpyHostToDevice, st) != hipSuccess) ||
-        (nk > 0 && hipMemcpyAsync(dv, v, nk * sizeof(float), hipMemcpyHostToDevice, st) != hipSuccess)) {
+    if (hipMemcpyAsync(dq, q, nq * esize, hipMemcpyHostToDevice, st) != hipSuccess ||
+        (nk > 0 && hipMemcpyAsync(dk, k, nk * esize, hipMemcpyHostToDevice, st) != hipSuccess) ||
+        (nk > 0 && hipMemcpyAsync(dv, v, nk * esize, hipMemcpyHostToDevice, st) != hipSuccess)) {
         (void)hipGetLastError();
         (void)hipStreamSynchronize(st);
         return FA_ERR_COPY;
@@ -427,8 +439,8 @@ int run_host(int variant, const float* q, const float* k, const float* v, size_t
     if (bh == 0 || sq == 0 || sk == 0 || d == 0) return FA_OK;   // out untouched
     if (!q || !k || !v || !out) return FA_ERR_INVALID_ARG;
     const int causal = cfg ? cfg->causal : 0;
-    return with_host_slices(q, k, v, bh, sq, sk, d, out,
-                            [&](hipStream_t st, const float* dq, const float* dk, const float* dv, float* dout) {
+    return with_host_slices(q, k, v, sizeof(float), bh, sq, sk, d, out,
+                            [&](hipStream_t st, const void* dq, const void* dk, const void* dv, float* dout) {
                                 return run_device(variant, st, dq, dk, dv, bh, sq, sk, d, causal, nullptr, dout);
                             });
 }
@@ -636,9 +648,11 @@ int fa_naive_attention(const float* q, size_t q_len, const float* k, size_t k_le
     if (rc != FA_OK) return rc;
     if (sq == 0 || d == 0) return FA_OK;
     if (!q || !out || (sk > 0 && (!k || !v))) return FA_ERR_INVALID_ARG;
-    return with_host_slices(q, k, v, 1, sq, sk, d, out,
-                            [&](hipStream_t st, const float* dq, const float* dk, const float* dv, float* dout) {
-                                return run_naive_device(st, dq, dk, dv, 1, sq, sk, d, causal, FA_NAIVE_F32, dout);
+    return with_host_slices(q, k, v, sizeof(float), 1, sq, sk, d, out,
+                            [&](hipStream_t st, const void* dq, const void* dk, const void* dv, float* dout) {
+                                return run_naive_device(st, static_cast<const float*>(dq), static_cast<const float*>(dk),
+                                                        static_cast<const float*>(dv), 1, sq, sk, d, causal,
+                                                        FA_NAIVE_F32, dout);
                             });
 }
 
@@ -652,8 +666,37 @@ int fa_device_ex(int variant, void* stream, const float* q, const float* k, cons
                  size_t heads, size_t sq, size_t sk, size_t d, const fa_config* cfg, const fa_launch_opts* opts,
                  float* out) {
     if (variant < 1 || variant > 3) return FA_ERR_INVALID_ARG;
+    if (opts && opts->dtype != FA_DTYPE_F32) return FA_ERR_INVALID_ARG;   // 16-bit inputs: fa_device_lp
     return run_device(variant, static_cast<hipStream_t>(stream), q, k, v, batch * heads, sq, sk, d,
                       cfg ? cfg->causal : 0, opts, out);
+}
+
+int fa_device_lp(int dtype, void* stream, const void* q, const void* k, const void* v, size_t batch, size_t heads,
+                 size_t sq, size_t sk, size_t d, const fa_config* cfg, const fa_launch_opts* opts, float* out) {
+    if (dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F16) return FA_ERR_INVALID_ARG;
+    fa_launch_opts o = opts ? *opts : fa_launch_opts{0.0f, FA_PATH_AUTO, 0, dtype};
+    o.dtype = dtype;
+    return run_device(3, static_cast<hipStream_t>(stream), q, k, v, batch * heads, sq, sk, d, cfg ? cfg->causal : 0,
+                      &o, out);
+}
+
+int fa_multihead_lp(int dtype, const void* q, size_t q_len, const void* k, size_t k_len, const void* v,
+                    size_t v_len, size_t batch, size_t heads, size_t sq, size_t sk, size_t d, const fa_config* cfg,
+                    float* out, size_t out_len) {
+    if (dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F16) return FA_ERR_INVALID_ARG;
+    const size_t bh = batch * heads;
+    if (q_len != bh * sq * d) return FA_ERR_Q_SHAPE;
+    if (k_len != bh * sk * d) return FA_ERR_K_SHAPE;
+    if (v_len != bh * sk * d) return FA_ERR_V_SHAPE;
+    if (out_len != bh * sq * d) return FA_ERR_OUT_SHAPE;
+    if (bh == 0 || sq == 0 || sk == 0 || d == 0) return FA_OK;   // out untouched
+    if (!q || !k || !v || !out) return FA_ERR_INVALID_ARG;
+    const int causal = cfg ? cfg->causal : 0;
+    const fa_launch_opts o{0.0f, FA_PATH_AUTO, 0, dtype};
+    return with_host_slices(q, k, v, 2, bh, sq, sk, d, out,
+                            [&](hipStream_t st, const void* dq, const void* dk, const void* dv, float* dout) {
+                                return run_device(3, st, dq, dk, dv, bh, sq, sk, d, causal, &o, dout);
+                            });
 }
 
 int fa_describe_launch(int variant, size_t batch, size_t heads, size_t sq, size_t sk, size_t d, int causal,

@@ -1230,3 +1230,5 @@ FA_MERGE(256)
     extern "C" __global__ void __launch_bounds__(256) fa_naive_pv_##SUF(NaiveParams p) { naive_pv_body<T>(p); }
 FA_NAIVE(float, f32)
 FA_NAIVE(double, f64)
+
+#include "fa_lp.inc"

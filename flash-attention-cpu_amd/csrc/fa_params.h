@@ -57,6 +57,9 @@ constexpr int fa_prefill_waves(int D) { return D <= 128 ? FA_PREFILL_WAVES : 8; 
 constexpr int fa_prefill_rows(int D) { return 16 * fa_prefill_waves(D); }
 // d = 256: v3 keeps two stages resident and fits its registers only with
 // 16-key stages; v1/v2 (one stage) use 32.
+// Low-precision (bf16 / f16) prefill: 8 waves x 16 rows, 64-key stages.
+constexpr int fa_lp_rows() { return 128; }
+constexpr int fa_lp_stage_keys() { return 64; }
 constexpr int fa_prefill_stage_keys(int D, int variant) {
     return D <= 128 ? (fa_prefill_waves(D) == 8 ? 64 : 32) : (variant == 3 ? 16 : 32);
 }

@@ -53,12 +53,17 @@ PATH_SPLITKV = 2
 NAIVE_F32 = 0
 NAIVE_F64 = 1
 
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+DTYPE_F16 = 2
+
 # Every symbol include/fa_hip.h declares.
 EXPORTED_SYMBOLS = (
     "fa_status_string", "fa_config_default",
     "fa_v1", "fa_v2", "fa_v3", "fa_attention",
     "fa_multihead_v1", "fa_multihead_v2", "fa_multihead_v3", "fa_attention_multihead",
     "fa_device_v1", "fa_device_v2", "fa_device_v3", "fa_device_ex",
+    "fa_device_lp", "fa_multihead_lp",
     "fa_naive_attention", "fa_naive_device",
     "fa_init", "fa_describe_launch",
 )
@@ -91,7 +96,8 @@ class _CConfig(ctypes.Structure):
 
 
 class _COpts(ctypes.Structure):
-    _fields_ = [("softmax_scale", ctypes.c_float), ("path", ctypes.c_int), ("num_splits", ctypes.c_int)]
+    _fields_ = [("softmax_scale", ctypes.c_float), ("path", ctypes.c_int), ("num_splits", ctypes.c_int),
+                ("dtype", ctypes.c_int)]
 
 
 _lib = None
@@ -145,6 +151,12 @@ def lib() -> ctypes.CDLL:
     L.fa_device_ex.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                ctypes.c_void_p, _SZ, _SZ, _SZ, _SZ, _SZ, _CFG, _OPTS, ctypes.c_void_p]
     L.fa_device_ex.restype = ctypes.c_int
+    L.fa_device_lp.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                               _SZ, _SZ, _SZ, _SZ, _SZ, _CFG, _OPTS, ctypes.c_void_p]
+    L.fa_device_lp.restype = ctypes.c_int
+    L.fa_multihead_lp.argtypes = [ctypes.c_int, ctypes.c_void_p, _SZ, ctypes.c_void_p, _SZ, ctypes.c_void_p, _SZ,
+                                  _SZ, _SZ, _SZ, _SZ, _SZ, _CFG, _F, _SZ]
+    L.fa_multihead_lp.restype = ctypes.c_int
     L.fa_naive_attention.argtypes = [_F, _SZ, _F, _SZ, _F, _SZ, _SZ, _SZ, _SZ, ctypes.c_int, _F, _SZ]
     L.fa_naive_attention.restype = ctypes.c_int
     L.fa_naive_device.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, _SZ, _SZ,
@@ -251,6 +263,53 @@ MULTIHEAD_VARIANTS = {1: flash_attention_multihead_v1, 2: flash_attention_multih
                       3: flash_attention_multihead_v3}
 
 
+def f32_to_bf16_bits(x) -> np.ndarray:
+    """Round f32 values to bfloat16 (nearest, ties to even); returns the 16-bit patterns."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    r = np.where(nan, (u >> 16) | 0x40, r)
+    return r.astype(np.uint16)
+
+
+def bf16_bits_to_f32(bits) -> np.ndarray:
+    """Widen bfloat16 patterns to f32 (exact)."""
+    return (np.ascontiguousarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def _in16(a, dtype: int) -> tuple[np.ndarray, int]:
+    want = np.uint16 if dtype == DTYPE_BF16 else np.float16
+    arr = np.ascontiguousarray(a)
+    if arr.dtype != want:
+        raise TypeError(f"16-bit inputs for dtype {dtype} must be numpy {np.dtype(want).name} "
+                        "(bfloat16 as uint16 bit patterns)")
+    return arr, arr.size
+
+
+def flash_attention_multihead_lp(dtype: int, q, k, v, batch, heads, seq_len_q, seq_len_k, d_head, config,
+                                 out) -> None:
+    """16-bit Q/K/V (DTYPE_BF16: uint16 bit patterns, DTYPE_F16: float16), f32 out (fa_multihead_lp)."""
+    q, nq = _in16(q, dtype)
+    k, nk = _in16(k, dtype)
+    v, nv = _in16(v, dtype)
+    out = _out(out)
+    cfg = _cfg(config)
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p) if a.size else None   # noqa: E731
+    _check(lib().fa_multihead_lp(int(dtype), ptr(q), nq, ptr(k), nk, ptr(v), nv, batch, heads, seq_len_q,
+                                 seq_len_k, d_head, ctypes.byref(cfg), _ptr(out), out.size))
+
+
+def attention_device_lp(dtype: int, q_ptr: int, k_ptr: int, v_ptr: int, batch: int, heads: int, seq_len_q: int,
+                        seq_len_k: int, d_head: int, causal: bool, out_ptr: int, stream: int = 0,
+                        softmax_scale: float | None = None, path: int = PATH_AUTO, num_splits: int = 0) -> None:
+    """Queue a 16-bit-input call on device pointers (fa_device_lp); returns when queued."""
+    cfg = _CConfig(64, 128, 1 if causal else 0)
+    opts = _COpts(float(softmax_scale) if softmax_scale else 0.0, int(path), int(num_splits), int(dtype))
+    _check(lib().fa_device_lp(int(dtype), ctypes.c_void_p(stream), ctypes.c_void_p(q_ptr), ctypes.c_void_p(k_ptr),
+                              ctypes.c_void_p(v_ptr), batch, heads, seq_len_q, seq_len_k, d_head,
+                              ctypes.byref(cfg), ctypes.byref(opts), ctypes.c_void_p(out_ptr)))
+
+
 def naive_attention(q, k, v, seq_len_q, seq_len_k, d_head, causal, out) -> None:
     """naive_attention (src/naive.rs:14): materialised scores, on the GPU, f32."""
     q, nq = _in(q)
@@ -283,9 +342,9 @@ def attention_device(variant: int, q_ptr: int, k_ptr: int, v_ptr: int, batch: in
 
 
 def describe_launch(variant: int, batch: int, heads: int, seq_len_q: int, seq_len_k: int, d_head: int,
-                    causal: bool, path: int = PATH_AUTO, num_splits: int = 0) -> str:
+                    causal: bool, path: int = PATH_AUTO, num_splits: int = 0, dtype: int = DTYPE_F32) -> str:
     """Kernel name(s) and grid a call would launch (launches nothing)."""
-    opts = _COpts(0.0, int(path), int(num_splits))
+    opts = _COpts(0.0, int(path), int(num_splits), int(dtype))
     buf = ctypes.create_string_buffer(512)
     _check(lib().fa_describe_launch(int(variant), batch, heads, seq_len_q, seq_len_k, d_head,
                                     1 if causal else 0, ctypes.byref(opts), buf, len(buf)))

@@ -140,15 +140,42 @@ int fa_device_v3(void* stream, const float* q, const float* k, const float* v, s
 #define FA_PATH_AUTO 0
 #define FA_PATH_PREFILL 1
 #define FA_PATH_SPLITKV 2
+/* Element type of Q, K, V (O is always f32). */
+#define FA_DTYPE_F32 0
+#define FA_DTYPE_BF16 1
+#define FA_DTYPE_F16 2
 typedef struct fa_launch_opts {
     float softmax_scale;
     int path;
     int num_splits;
+    int dtype;   /* FA_DTYPE_*: read by fa_describe_launch; fa_device_ex accepts only F32 */
 } fa_launch_opts;
 
 int fa_device_ex(int variant, void* stream, const float* q, const float* k, const float* v,
                  size_t batch, size_t heads, size_t seq_len_q, size_t seq_len_k, size_t d_head,
                  const fa_config* config, const fa_launch_opts* opts, float* out);
+
+/* ---- 16-bit inputs (bf16 / f16) -------------------------------------------
+ * Not in the reference, whose roadmap plans bf16 dot products with f32
+ * accumulation (ROADMAP.md, item 2 "bf16 dot-product acceleration").  Q, K, V
+ * hold bfloat16 (FA_DTYPE_BF16, raw 16-bit patterns) or IEEE binary16
+ * (FA_DTYPE_F16) in the layout of the f32 entry points; O is f32.  QK^T and PV
+ * run on 16-bit MFMA with f32 accumulation (every product exact), the softmax
+ * in f32, and the probabilities are rounded to the input type for PV, so
+ * each output element is within u * max|V| of f32 attention on the same
+ * 16-bit inputs (u = 2^-8 bf16, 2^-11 f16).  Causal masking, shape checks and
+ * zero-dimension behaviour are those of fa_multihead_v2; d_head <= 256.  The
+ * algorithm is v2/v3's (deferred normalisation, causal skip); no variant
+ * argument.  opts: softmax_scale, path (AUTO or PREFILL) and num_splits as
+ * for fa_device_ex; opts->dtype is ignored. */
+int fa_device_lp(int dtype, void* stream, const void* q, const void* k, const void* v, size_t batch,
+                 size_t heads, size_t seq_len_q, size_t seq_len_k, size_t d_head,
+                 const fa_config* config, const fa_launch_opts* opts, float* out);
+/* Host-slice form; lengths count elements. */
+int fa_multihead_lp(int dtype, const void* q, size_t q_len, const void* k, size_t k_len,
+                    const void* v, size_t v_len, size_t batch, size_t heads, size_t seq_len_q,
+                    size_t seq_len_k, size_t d_head, const fa_config* config, float* out,
+                    size_t out_len);
 
 /* ---- naive attention (materialised scores) -------------------------------
  * naive_attention -- src/naive.rs:14-75: the textbook O(seq_q * seq_k)

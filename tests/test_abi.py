@@ -174,8 +174,8 @@ def test_bad_code_object_path_fails_with_module_or_no_device():
     assert out == str(expect)
 
 
-def describe(variant, b, h, sq, sk, d, causal, path=fa.PATH_AUTO, splits=0):
-    return fa.describe_launch(variant, b, h, sq, sk, d, causal, path, splits)
+def describe(variant, b, h, sq, sk, d, causal, path=fa.PATH_AUTO, splits=0, dtype=fa.DTYPE_F32):
+    return fa.describe_launch(variant, b, h, sq, sk, d, causal, path, splits, dtype)
 
 
 def test_planning_prefill_kernels():
@@ -246,3 +246,33 @@ def test_cpp_mirror_header_compiles(tmp_path):
                    'return c.block_size_q == 64 ? 0 : 1; }\n' % hdr)
     subprocess.run(["g++", "-std=c++17", "-fsyntax-only", "-I", os.path.join(ROOT, "include"), str(src)],
                    check=True)
+
+
+def test_bf16_conversion_helpers():
+    x = np.array([1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -2.5, 3.14159, np.inf, -np.inf, 0.0, -0.0, 65504.0],
+                 np.float32)
+    bits = fa.f32_to_bf16_bits(x)
+    back = fa.bf16_bits_to_f32(bits)
+    # ties to even: 1 + 2^-8 -> 1, 1 + 3*2^-8 -> 1 + 2^-6; specials kept
+    assert list(back[:3]) == [1.0, 1.0, 1.0 + 2 ** -6]
+    assert back[3] == -2.5 and abs(back[4] - 3.14159) < 2 ** -7 * 4
+    assert np.isposinf(back[5]) and np.isneginf(back[6]) and back[7] == 0.0 and np.signbit(back[8])
+    assert np.isnan(fa.bf16_bits_to_f32(fa.f32_to_bf16_bits(np.array([np.nan], np.float32))))[0]
+    r = np.random.default_rng(0).standard_normal(1000).astype(np.float32)
+    assert np.array_equal(fa.f32_to_bf16_bits(fa.bf16_bits_to_f32(fa.f32_to_bf16_bits(r))), fa.f32_to_bf16_bits(r))
+    assert np.max(np.abs(fa.bf16_bits_to_f32(fa.f32_to_bf16_bits(r)) - r) / np.abs(r)) <= 2 ** -8
+
+
+def test_planning_16bit_inputs():
+    s = describe(3, 1, 32, 2048, 2048, 128, True, dtype=fa.DTYPE_BF16)
+    assert s.startswith("fa_prefill_lp_bf16_d128_2 grid=512x1x1 block=512")
+    assert describe(2, 1, 2, 100, 100, 40, False, dtype=fa.DTYPE_F16).startswith("fa_prefill_lp_f16_d64_2")
+    assert describe(2, 1, 2, 100, 100, 20, False, dtype=fa.DTYPE_F16).startswith("fa_prefill_lp_f16_d32_0")
+    assert "fa_decode" not in describe(3, 1, 32, 1, 32768, 128, False, dtype=fa.DTYPE_BF16)   # key split instead
+    assert "fa_merge_d128" in describe(3, 1, 32, 1, 32768, 128, False, dtype=fa.DTYPE_BF16)
+    with pytest.raises(fa.FaError) as e:
+        describe(3, 1, 1, 4, 512, 64, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_BF16)
+    assert e.value.status == fa.FA_ERR_INVALID_ARG
+    with pytest.raises(fa.FaError) as e:
+        describe(3, 1, 1, 4, 512, 64, False, dtype=7)
+    assert e.value.status == fa.FA_ERR_INVALID_ARG

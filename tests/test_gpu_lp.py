@@ -1,0 +1,198 @@
+"""GPU parity of the 16-bit-input path (fa_device_lp / fa_multihead_lp).
+
+Reference: the oracle's CPU v2 (and the f64 GPU naive at full size) on the
+same inputs widened to f32, which is exact.  The kernel's products are exact
+and its sums f32; the one deliberate rounding is the probabilities, rounded to
+the input type for the PV product, which moves each output element by at most
+u * max|V| (u = 2^-8 bf16, 2^-11 f16: |sum_j (p^_j - p_j) v_j| / l <=
+u * sum_j p_j |v_j| / l).  The bar: max-abs <= u * max|V| + 2e-5 and
+relative L2 <= u.  Known answers that involve no rounding (a row that sees
+one key returns that key's V row) are checked bit for bit.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import flash_attention_amd as fa
+import oracle
+from fa_testutil import max_abs_diff, normal_vec, rel_l2, uniform_vec
+
+pytestmark = pytest.mark.gpu
+
+U = {fa.DTYPE_BF16: 2.0 ** -8, fa.DTYPE_F16: 2.0 ** -11}   # unit roundoff
+NAME = {fa.DTYPE_BF16: "bf16", fa.DTYPE_F16: "f16"}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    fa.init()
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def to16(x32: np.ndarray, dtype: int):
+    """(16-bit array for the library, its exact f32 widening)."""
+    if dtype == fa.DTYPE_BF16:
+        bits = fa.f32_to_bf16_bits(x32)
+        return bits, fa.bf16_bits_to_f32(bits)
+    h = np.asarray(x32, dtype=np.float32).astype(np.float16)
+    return h, h.astype(np.float32)
+
+
+def lp_device(dtype, q16, k16, v16, bh, sq, sk, d, causal, path=fa.PATH_AUTO, splits=0, guard=64, misalign=False):
+    """fa_device_lp on copies of the 16-bit inputs; sentinels around O."""
+    torch = _torch()
+    dev = torch.device("cuda", 0)
+
+    def dev16(a):
+        t = torch.from_numpy(a.view(np.int16).copy()).to(dev)
+        if misalign:   # a 2-byte offset forces the register-staged loader
+            buf = torch.zeros(a.size + 1, dtype=torch.int16, device=dev)
+            buf[1:] = t
+            return buf, buf[1:].data_ptr()
+        return t, t.data_ptr()
+
+    (tq, pq), (tk, pk), (tv, pv) = dev16(q16), dev16(k16), dev16(v16)
+    buf = torch.full((bh * sq * d + 2 * guard,), 12.5, device=dev)
+    out = buf[guard:guard + bh * sq * d]
+    fa.attention_device_lp(dtype, pq, pk, pv, 1, bh, sq, sk, d, causal, out.data_ptr(),
+                           torch.cuda.current_stream().cuda_stream, path=path, num_splits=splits)
+    torch.cuda.synchronize()
+    host = buf.cpu().numpy()
+    assert np.all(host[:guard] == 12.5) and np.all(host[-guard:] == 12.5), "write outside out"
+    return host[guard:guard + bh * sq * d]
+
+
+def assert_lp(got, want, v32, dtype, what):
+    u = U[dtype]
+    tol = u * float(np.max(np.abs(v32))) + 2e-5
+    ma, rl = max_abs_diff(got, want), rel_l2(got, want)
+    print(f"[lp-parity] {what}: max-abs {ma:.3g} (bound {tol:.3g}) rel-L2 {rl:.3g} (bound {u:.3g})", flush=True)
+    assert ma <= tol, (what, ma, tol)
+    assert rl <= u, (what, rl, u)
+
+
+CASES = [(1, 1, 1, 8, False), (2, 64, 64, 64, False), (3, 100, 37, 128, True), (1, 37, 100, 256, False),
+         (2, 300, 300, 32, True), (1, 129, 200, 96, False), (2, 257, 513, 128, True), (1, 700, 300, 64, True),
+         (1, 17, 1000, 40, False), (2, 200, 200, 17, True), (1, 150, 90, 200, False), (1, 1000, 1000, 128, True)]
+
+
+@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16])
+def test_lp_matches_oracle_on_widened_inputs(dtype):
+    rng = np.random.default_rng(31)
+    for bh, sq, sk, d, causal in CASES:
+        q16, q32 = to16(rng.standard_normal(bh * sq * d, dtype=np.float32), dtype)
+        k16, k32 = to16(rng.standard_normal(bh * sk * d, dtype=np.float32), dtype)
+        v16, v32 = to16(rng.standard_normal(bh * sk * d, dtype=np.float32), dtype)
+        want = oracle.run(2, q32, k32, v32, bh, sq, sk, d, causal, 64, 128)
+        what = f"{NAME[dtype]} {bh}x{sq}x{sk} d={d} causal={causal}"
+        print("[case]", what, fa.describe_launch(3, 1, bh, sq, sk, d, causal, dtype=dtype), flush=True)
+        got = lp_device(dtype, q16, k16, v16, bh, sq, sk, d, causal)
+        assert_lp(got, want, v32, dtype, what)
+        if d % 8 == 0:   # the register-staged loader on the same inputs
+            got2 = lp_device(dtype, q16, k16, v16, bh, sq, sk, d, causal, misalign=True)
+            assert_lp(got2, want, v32, dtype, what + " (misaligned)")
+
+
+@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16])
+def test_lp_every_head_dim(dtype):
+    rng = np.random.default_rng(5)
+    for d in list(range(1, 33)) + [48, 63, 64, 65, 100, 127, 128, 129, 192, 255, 256]:
+        bh, sq, sk = 1, 70, 90
+        q16, q32 = to16(rng.uniform(-1, 1, bh * sq * d).astype(np.float32), dtype)
+        k16, k32 = to16(rng.uniform(-1, 1, bh * sk * d).astype(np.float32), dtype)
+        v16, v32 = to16(rng.uniform(-1, 1, bh * sk * d).astype(np.float32), dtype)
+        for causal in (False, True):
+            want = oracle.run(2, q32, k32, v32, bh, sq, sk, d, causal, 64, 128)
+            got = lp_device(dtype, q16, k16, v16, bh, sq, sk, d, causal)
+            assert_lp(got, want, v32, dtype, f"{NAME[dtype]} d={d} causal={causal}")
+
+
+@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16])
+def test_lp_known_answers_are_exact(dtype):
+    rng = np.random.default_rng(9)
+    bh, s, d = 2, 300, 128
+    q16, _ = to16(rng.standard_normal(bh * s * d, dtype=np.float32), dtype)
+    k16, _ = to16(rng.standard_normal(bh * s * d, dtype=np.float32), dtype)
+    v16, v32 = to16(rng.standard_normal(bh * s * d, dtype=np.float32), dtype)
+    # causal row 0 sees only key 0: p = 1 exactly, O row 0 = V row 0 (tests/correctness.rs:240-263)
+    out = lp_device(dtype, q16, k16, v16, bh, s, s, d, True).reshape(bh, s, d)
+    for h in range(bh):
+        assert np.array_equal(out[h, 0], v32.reshape(bh, s, d)[h, 0])
+    # one key: every row is V[0]
+    out1 = lp_device(dtype, q16, k16[:bh * d].copy(), v16[:bh * d].copy(), bh, s, 1, d, False).reshape(bh, s, d)
+    for h in range(bh):   # head h's single key/value row is element block h of the first bh*d
+        assert np.array_equal(out1[h], np.tile(v32[h * d:(h + 1) * d], (s, 1)))
+
+
+@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16])
+def test_lp_key_split_and_determinism(dtype):
+    rng = np.random.default_rng(12)
+    for bh, sq, sk, d, causal in [(1, 1000, 1000, 256, True), (2, 300, 2000, 128, False), (3, 129, 1025, 64, True)]:
+        q16, q32 = to16(rng.standard_normal(bh * sq * d, dtype=np.float32), dtype)
+        k16, k32 = to16(rng.standard_normal(bh * sk * d, dtype=np.float32), dtype)
+        v16, v32 = to16(rng.standard_normal(bh * sk * d, dtype=np.float32), dtype)
+        want = oracle.run(2, q32, k32, v32, bh, sq, sk, d, causal, 64, 128)
+        for splits in (2, 5, 16):
+            got = lp_device(dtype, q16, k16, v16, bh, sq, sk, d, causal, fa.PATH_PREFILL, splits)
+            assert_lp(got, want, v32, dtype, f"{NAME[dtype]} split={splits} {bh}x{sq}x{sk} d={d}")
+        a = lp_device(dtype, q16, k16, v16, bh, sq, sk, d, causal)
+        b = lp_device(dtype, q16, k16, v16, bh, sq, sk, d, causal)
+        assert np.array_equal(a, b)
+        assert_lp(a, want, v32, dtype, f"{NAME[dtype]} auto {bh}x{sq}x{sk} d={d}")
+
+
+def test_lp_host_slices_shape_errors_and_zero_dims():
+    dtype = fa.DTYPE_BF16
+    rng = np.random.default_rng(2)
+    bh, sq, sk, d = 2, 33, 65, 64
+    q16, q32 = to16(rng.standard_normal(bh * sq * d, dtype=np.float32), dtype)
+    k16, k32 = to16(rng.standard_normal(bh * sk * d, dtype=np.float32), dtype)
+    v16, v32 = to16(rng.standard_normal(bh * sk * d, dtype=np.float32), dtype)
+    out = np.zeros(bh * sq * d, np.float32)
+    fa.flash_attention_multihead_lp(dtype, q16, k16, v16, 1, bh, sq, sk, d, fa.FlashAttentionConfig(causal=True), out)
+    assert_lp(out, oracle.run(2, q32, k32, v32, bh, sq, sk, d, True, 64, 128), v32, dtype, "host slices")
+    f16q, _ = to16(rng.standard_normal(bh * sq * d, dtype=np.float32), fa.DTYPE_F16)
+    with pytest.raises(TypeError):
+        fa.flash_attention_multihead_lp(dtype, f16q, k16, v16, 1, bh, sq, sk, d, None, out)
+    for args, msg in [((q16[:-1], k16, v16, out), "q shape"), ((q16, k16[:-1], v16, out), "k shape"),
+                      ((q16, k16, v16[:-1], out), "v shape"), ((q16, k16, v16, out[:-1]), "out shape")]:
+        with pytest.raises(fa.ShapeMismatch, match=msg):
+            fa.flash_attention_multihead_lp(dtype, args[0], args[1], args[2], 1, bh, sq, sk, d, None, args[3])
+    keep = np.full(sq * d, 7.0, np.float32)
+    fa.flash_attention_multihead_lp(dtype, q16[:sq * d], np.zeros(0, np.uint16), np.zeros(0, np.uint16), 1, 1, sq,
+                                    0, d, None, keep)
+    assert np.all(keep == 7.0)
+
+
+@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16])
+def test_lp_full_size_configs_against_naive_f64(dtype):
+    """Configs 2 and 5 at full size, every row, against the f64 GPU naive on the widened inputs."""
+    torch = _torch()
+    dev = torch.device("cuda", 0)
+    for name, (bh, sq, sk, d, causal, sig, vu) in {"config2": (32, 2048, 2048, 128, True, 1.0, False),
+                                                   "config5": (16, 4096, 1024, 256, False, 3.0, True)}.items():
+        q16, q32 = to16(normal_vec(bh * sq * d, 1, sig), dtype)
+        k16, k32 = to16(normal_vec(bh * sk * d, 2, sig), dtype)
+        v16, v32 = to16(uniform_vec(bh * sk * d, 3) if vu else normal_vec(bh * sk * d, 3), dtype)
+        tq, tk, tv = (torch.from_numpy(a).to(dev) for a in (q32, k32, v32))
+        ref = torch.empty(bh * sq * d, device=dev)
+        st = torch.cuda.current_stream().cuda_stream
+        fa.naive_device(tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), 1, bh, sq, sk, d, causal, ref.data_ptr(), st,
+                        fa.NAIVE_F64)
+        del tq, tk, tv
+        t16 = [torch.from_numpy(a.view(np.int16).copy()).to(dev) for a in (q16, k16, v16)]
+        out = torch.full((bh * sq * d,), 12.5, device=dev)
+        fa.attention_device_lp(dtype, t16[0].data_ptr(), t16[1].data_ptr(), t16[2].data_ptr(), 1, bh, sq, sk, d,
+                               causal, out.data_ptr(), st)
+        torch.cuda.synchronize()
+        diff = (out - ref).abs().max().item()
+        rl = ((out.double() - ref.double()).norm() / ref.double().norm()).item()
+        tol = U[dtype] * float(np.max(np.abs(v32))) + 2e-5
+        print(f"[lp-naive-f64] {NAME[dtype]} {name}: max-abs {diff:.3g} (bound {tol:.3g}) rel-L2 {rl:.3g}",
+              flush=True)
+        assert diff <= tol and rl <= U[dtype], (name, diff, rl)
