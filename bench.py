@@ -31,6 +31,7 @@ sys.path.insert(0, os.path.join(ROOT, "flash-attention-cpu_amd"))
 METRIC = "attention TFLOP/s f32 (32h×2048×d128 causal) + % FP32-MFMA peak; decode GB/s"
 PEAK_TFLOPS = 157.3     # MI355X dense FP32 MFMA
 PEAK_GBS = 8000.0       # MI355X HBM3E
+PEAK_TFLOPS_16 = 2500.0  # MI355X dense bf16 / f16 MFMA
 
 
 def log(msg: str) -> None:
@@ -269,6 +270,49 @@ def main() -> int:
         del wl
     del k_dec, v_dec
     torch.cuda.empty_cache()
+
+    # 16-bit inputs (fa_device_lp): config 2 and the decode shape, same seeds,
+    # rounded to bf16 / f16; FLOP against the 16-bit MFMA peak, bytes at 2 B.
+    for name, dt, tdt in ((() if args.only_config2 else (("bf16", fa.DTYPE_BF16, torch.bfloat16),
+                                                          ("f16", fa.DTYPE_F16, torch.float16)))):
+        for tag, wl in (("config2", head), ("config4_decode_sq1", None)):
+            if wl is None:
+                wl = Workload(torch, "config4 seq_q=1", 32, 1, 32768, 128, False)
+            lq, lk, lv = wl.q.to(tdt), wl.k.to(tdt), wl.v.to(tdt)
+            stream = torch.cuda.current_stream()
+
+            def call_lp():
+                fa.attention_device_lp(dt, lq.data_ptr(), lk.data_ptr(), lv.data_ptr(), 1, wl.bh, wl.sq, wl.sk,
+                                       wl.d, wl.causal, wl.o.data_ptr(), stream.cuda_stream)
+
+            t_ramp = time.perf_counter()
+            while time.perf_counter() - t_ramp < RAMP_SECONDS:
+                for _ in range(8):
+                    call_lp()
+                torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            n = max(10, args.steps)
+            e0.record(stream)
+            for _ in range(n):
+                call_lp()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / n
+            ent = {"us_per_call": round(ms * 1e3, 1),
+                   "kernels": fa.describe_launch(3, 1, wl.bh, wl.sq, wl.sk, wl.d, wl.causal, dtype=dt)}
+            if tag == "config2":
+                tf = wl.flops / (ms * 1e-3) / 1e12
+                ent.update(tflops=round(tf, 1), pct_16bit_mfma_peak=round(100 * tf / PEAK_TFLOPS_16, 1))
+            else:
+                lp_bytes = wl.bh * wl.d * (2 * wl.sq + 4 * wl.sk + 4 * wl.sq)   # 16-bit Q, K, V; f32 O
+                gbs = lp_bytes / (ms * 1e-3) / 1e9
+                ent.update(gbs=round(gbs, 1), pct_hbm_peak=round(100 * gbs / PEAK_GBS, 1))
+            extra[f"{tag}_{name}"] = ent
+            log(f"[bench] {tag} {name}: {ent}")
+            del lq, lk, lv
+            if tag != "config2":
+                del wl
+        torch.cuda.empty_cache()
 
     if args.all:
         for name, shape in (("config1", (1, 256, 256, 64, False, 1.0, False)),

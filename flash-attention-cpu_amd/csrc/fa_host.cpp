@@ -196,10 +196,15 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     if (!split) {
         if (nqb * bh > imax) return FA_ERR_UNSUPPORTED;
         p.nqb = static_cast<int>(nqb);
+        int lp_tiles = 1;
         if (lp) {
+            // Two 16-row tiles per wave halve LDS traffic per row but leave one
+            // wave per SIMD in a workgroup running alone: worth it at D = 128
+            // unless the grid is a single round of unequal causal blocks.
+            if (D == 128 && (!causal || nqb * bh > 2 * (size_t)num_cus)) lp_tiles = 2;
             // 0: register-staged scalar loads (any d), 2: global->LDS DMA
-            std::snprintf(buf, sizeof(buf), "fa_prefill_lp_%s_d%d_%d", dtype == FA_DTYPE_BF16 ? "bf16" : "f16", D,
-                          vec ? 2 : 0);
+            std::snprintf(buf, sizeof(buf), "fa_prefill_lp_%s_d%d_%d_t%d", dtype == FA_DTYPE_BF16 ? "bf16" : "f16",
+                          D, vec ? 2 : 0, lp_tiles);
         } else {
             // 0: scalar loads (any d), 1: 128-bit loads, 2: global->LDS DMA (v3)
             const int loader = vec ? (variant == 3 ? 2 : 1) : 0;
@@ -207,7 +212,10 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
         }
         plan->first.name = buf;
         plan->first.gx = static_cast<unsigned>(nqb * bh);
-        plan->first.bx = lp ? 512 : 64 * fa_prefill_waves(D);
+        plan->first.bx = 64 * (lp ? fa_lp_waves(lp_tiles) : fa_prefill_waves(D));
+        // The 16-bit kernels fit two workgroups per CU for D <= 128.
+        if (lp && D <= 128 && causal && bh <= (size_t)num_cus && num_cus % bh == 0)
+            p.pair_w = static_cast<int>(num_cus / bh);
         plan->ws_floats = 0;
         // Key split for v2/v3 when the grid would leave CUs idle: a query
         // block's keys are cut into splits of `per` stages, one workgroup
@@ -271,6 +279,7 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
                 p.split_len = static_cast<int>(per * SKs);
                 p.ks_rows = static_cast<int>(rows);
                 p.merge_scale = 1.0f;   // prefill partial maxima are in the log2 domain
+                p.pair_w = 0;           // the compact split grid has its own order
                 size_t wgs = 0;   // compact grid: split y of every block that reaches it
                 for (size_t y = 0; y < nks; ++y) wgs += (causal ? nqb - std::min(nqb, y * per * SKs / rows) : nqb) * bh;
                 if (wgs > imax) return FA_ERR_UNSUPPORTED;

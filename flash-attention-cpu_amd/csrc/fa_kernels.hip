@@ -100,6 +100,13 @@ __device__ __forceinline__ void map_block(const FaParams& p, int x, int& qb, int
         bh = x % p.bh;
         rank = x / p.bh;
     }
+    if (p.pair_w > 0) {
+        // With two resident workgroups per CU, workgroups x and x + #CUs share
+        // a CU; reversing every second round of ranks pairs the k-th longest
+        // causal block with the k-th shortest.
+        const int round = rank / p.pair_w, w_eff = min(p.pair_w, p.nqb - round * p.pair_w);
+        if (round & 1) rank = round * p.pair_w + (w_eff - 1 - rank % p.pair_w);
+    }
     qb = p.causal ? (p.nqb - 1 - rank) : rank;
 }
 

@@ -27,6 +27,9 @@ typedef struct FaParams {
     int ks_rows;         // key split: query rows per prefill block (0: split-KV decode)
     float merge_scale;   // fa_merge: factor taking partial maxima to the log2 domain
                          // (split-KV: scale_log2e; prefill key split: 1, already scaled)
+    int pair_w;          // prefill, two workgroups per CU: causal ranks per dispatch round
+                         // (odd rounds run in reverse so each CU pairs a long and a short
+                         // block); 0 = plain longest-first order
 } FaParams;
 
 
@@ -57,8 +60,10 @@ constexpr int fa_prefill_waves(int D) { return D <= 128 ? FA_PREFILL_WAVES : 8; 
 constexpr int fa_prefill_rows(int D) { return 16 * fa_prefill_waves(D); }
 // d = 256: v3 keeps two stages resident and fits its registers only with
 // 16-key stages; v1/v2 (one stage) use 32.
-// Low-precision (bf16 / f16) prefill: 8 waves x 16 rows, 64-key stages.
+// Low-precision (bf16 / f16) prefill: 128-row workgroups of waves owning MT
+// 16-row tiles each (MT = 1, or 2 for D = 128); 64-key stages.
 constexpr int fa_lp_rows() { return 128; }
+constexpr int fa_lp_waves(int MT) { return fa_lp_rows() / (16 * MT); }
 constexpr int fa_lp_stage_keys() { return 64; }
 constexpr int fa_prefill_stage_keys(int D, int variant) {
     return D <= 128 ? (fa_prefill_waves(D) == 8 ? 64 : 32) : (variant == 3 ? 16 : 32);

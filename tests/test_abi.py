@@ -265,9 +265,12 @@ def test_bf16_conversion_helpers():
 
 def test_planning_16bit_inputs():
     s = describe(3, 1, 32, 2048, 2048, 128, True, dtype=fa.DTYPE_BF16)
-    assert s.startswith("fa_prefill_lp_bf16_d128_2 grid=512x1x1 block=512")
-    assert describe(2, 1, 2, 100, 100, 40, False, dtype=fa.DTYPE_F16).startswith("fa_prefill_lp_f16_d64_2")
-    assert describe(2, 1, 2, 100, 100, 20, False, dtype=fa.DTYPE_F16).startswith("fa_prefill_lp_f16_d32_0")
+    assert s.startswith("fa_prefill_lp_bf16_d128_2_t1 grid=512x1x1 block=512")   # one round, causal: 1 tile/wave
+    assert describe(3, 1, 32, 2048, 2048, 128, False, dtype=fa.DTYPE_BF16).startswith(
+        "fa_prefill_lp_bf16_d128_2_t2 grid=512x1x1 block=256")
+    assert describe(3, 1, 8, 16384, 16384, 128, True, dtype=fa.DTYPE_BF16).startswith("fa_prefill_lp_bf16_d128_2_t2")
+    assert describe(2, 1, 2, 100, 100, 40, False, dtype=fa.DTYPE_F16).startswith("fa_prefill_lp_f16_d64_2_t1")
+    assert describe(2, 1, 2, 100, 100, 20, False, dtype=fa.DTYPE_F16).startswith("fa_prefill_lp_f16_d32_0_t1")
     assert "fa_decode" not in describe(3, 1, 32, 1, 32768, 128, False, dtype=fa.DTYPE_BF16)   # key split instead
     assert "fa_merge_d128" in describe(3, 1, 32, 1, 32768, 128, False, dtype=fa.DTYPE_BF16)
     with pytest.raises(fa.FaError) as e:
