@@ -142,6 +142,7 @@ int pad_d(size_t d) {
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
 int make_plan(int variant, const void* q, const void* k, const void* v, const float* out,
               size_t bh, size_t sq, size_t sk, size_t d, int causal, const fa_launch_opts* opts,
@@ -152,7 +153,7 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     if (dtype != FA_DTYPE_F32 && dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F16) return FA_ERR_INVALID_ARG;
     const bool lp = dtype != FA_DTYPE_F32;   // 16-bit inputs: the fa_prefill_lp kernels
     if (path < FA_PATH_AUTO || path > FA_PATH_SPLITKV) return FA_ERR_INVALID_ARG;
-    if (path == FA_PATH_SPLITKV && (variant == 1 || lp)) return FA_ERR_INVALID_ARG;
+    if (path == FA_PATH_SPLITKV && variant == 1) return FA_ERR_INVALID_ARG;
     if (opts && opts->num_splits < 0) return FA_ERR_INVALID_ARG;
     if (d > (size_t)kMaxD) return FA_ERR_UNSUPPORTED;
     const size_t imax = 0x7fffffff;
@@ -180,10 +181,13 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     const size_t nqb = (sq + rows - 1) / rows;
     const size_t nqt = (sq + kDecodeRows - 1) / kDecodeRows;
     bool split = false;
-    if (variant != 1 && !lp) {
+    if (variant != 1) {
         if (path == FA_PATH_SPLITKV) {
             split = true;
-        } else if (path == FA_PATH_AUTO) {
+        } else if (path == FA_PATH_AUTO && !lp) {
+            // (16-bit inputs: the key-split 16-bit prefill is faster than the
+            // widening split-KV kernel -- 113 vs 148 us on config 4 -- so AUTO
+            // keeps the prefill; FA_PATH_SPLITKV still selects the decode.)
             split = sq <= 64 && sk >= 512 && nqb * bh < (size_t)num_cus;
         }
     }
@@ -300,7 +304,9 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     if (opts && opts->num_splits > 0) {
         nsplit = (size_t)opts->num_splits;
     } else {
-        const size_t wg_per_cu = 2;   // 8 waves per CU at the decode kernel's register use
+        // resident decode workgroups per CU at the kernel's register use
+        // (D = 256: one, with 424 of 512 registers per lane)
+        const size_t wg_per_cu = D <= 128 ? 2 : 1;
         const size_t slots = wg_per_cu * (size_t)num_cus;
         nsplit = slots / (nqt * bh);
         if (nsplit < 1) nsplit = 1;
@@ -314,7 +320,14 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     p.num_splits = static_cast<int>(nsplit);
     p.split_len = static_cast<int>(split_len);
     p.merge_scale = p.scale_log2e;   // decode partial maxima are raw scores
-    std::snprintf(buf, sizeof(buf), "fa_decode_d%d_%d", D, vec ? 1 : 0);
+    if (lp) {
+        // 16-bit K/V streamed and widened in registers: 8-byte loads need d % 4 == 0
+        const bool vec8 = (d % 4 == 0) && aligned8(q) && aligned8(k) && aligned8(v) && aligned16(out);
+        std::snprintf(buf, sizeof(buf), "fa_decode_%s_d%d_%d", dtype == FA_DTYPE_BF16 ? "bf16" : "f16", D,
+                      vec8 ? 1 : 0);
+    } else {
+        std::snprintf(buf, sizeof(buf), "fa_decode_d%d_%d", D, vec ? 1 : 0);
+    }
     plan->first.name = buf;
     plan->first.gx = static_cast<unsigned>(nsplit);
     plan->first.gy = static_cast<unsigned>(nqt);

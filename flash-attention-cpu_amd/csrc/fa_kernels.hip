@@ -85,6 +85,57 @@ __device__ __forceinline__ f32x4 load4(const float* __restrict__ base, int row, 
     return v;
 }
 
+// Decode operand registers: f32x4 for f32 inputs; for 16-bit inputs the raw
+// 4 elements, widened to f32 (exactly) only where the MFMA consumes them, so
+// a prefetch does not wait for its load.
+template <typename E>
+struct RawOf {
+    typedef E type __attribute__((ext_vector_type(4)));
+};
+template <>
+struct RawOf<float> {
+    typedef f32x4 type;
+};
+template <typename E>
+__device__ __forceinline__ f32x4 widen(const typename RawOf<E>::type& r) {
+    if constexpr (std::is_same<E, float>::value) {
+        return r;
+    } else {
+        return (f32x4){static_cast<float>(r[0]), static_cast<float>(r[1]), static_cast<float>(r[2]),
+                       static_cast<float>(r[3])};
+    }
+}
+// load4 for any element type, raw (zero outside [0,nrows) x [0,d)).  VEC:
+// one 16-byte (f32) or 8-byte (16-bit) load; d % 4 == 0 and aligned rows.
+template <typename E, bool VEC, bool NT = false>
+__device__ __forceinline__ typename RawOf<E>::type load4r(const E* __restrict__ base, int row, int nrows, int col,
+                                                           int d) {
+    typedef typename RawOf<E>::type R;
+    if constexpr (std::is_same<E, float>::value) {
+        return load4<VEC, NT>(base, row, nrows, col, d);
+    } else {
+        R v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = E(0.0f);
+        if (row < nrows) {
+            const E* p = base + (size_t)row * d + col;
+            if (VEC) {
+                if (col < d) {
+                    unsigned long long bits;
+                    if constexpr (NT) bits = __builtin_nontemporal_load(reinterpret_cast<const unsigned long long*>(p));
+                    else bits = *reinterpret_cast<const unsigned long long*>(p);
+                    v = __builtin_bit_cast(R, bits);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (col + e < d) v[e] = p[e];
+            }
+        }
+        return v;
+    }
+}
+
 // Workgroup -> (query block, batch*head) with the longest causal blocks first
 // (greedy longest-processing-time order as workgroups retire) and, when bh is
 // a multiple of 8, all blocks of one head on the same XCD (workgroups are
@@ -728,8 +779,11 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
 // 4 waves merge through LDS into one partial (m, l, O) per workgroup, and
 // fa_merge combines the splits by log-sum-exp.
 // ---------------------------------------------------------------------------
-template <int D, bool VEC, bool DBUF>
+// E: element type of Q/K/V (float, or bf16 / f16 widened to f32 as loaded).
+// DBUF_REQ: double-buffer the K/V registers; D = 256 has no registers for it.
+template <int D, bool VEC, bool DBUF_REQ, typename E = float>
 __device__ __forceinline__ void decode_body(const FaParams& p) {
+    constexpr bool DBUF = DBUF_REQ && D <= 128;
     constexpr int NQ = D / 4;          // MFMA k-steps over d (16x16x4)
     constexpr int NKL = D / 16;        // 128-bit K loads per lane per 16 keys
     constexpr int NVL = D / 64 > 0 ? D / 64 : 1;  // 128-bit V loads per lane per key step
@@ -748,9 +802,9 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
     const int qt = blockIdx.y;
     const int bh = blockIdx.z;
     const int seq_q = p.seq_q, seq_k = p.seq_k, d = p.d;
-    const float* __restrict__ Qh = p.q + (size_t)bh * seq_q * d;
-    const float* __restrict__ Kh = p.k + (size_t)bh * seq_k * d;
-    const float* __restrict__ Vh = p.v + (size_t)bh * seq_k * d;
+    const E* __restrict__ Qh = reinterpret_cast<const E*>(p.q) + (size_t)bh * seq_q * d;
+    const E* __restrict__ Kh = reinterpret_cast<const E*>(p.k) + (size_t)bh * seq_k * d;
+    const E* __restrict__ Vh = reinterpret_cast<const E*>(p.v) + (size_t)bh * seq_k * d;
     const float c = p.scale_log2e;
     const bool causal = p.causal != 0;
 
@@ -768,7 +822,7 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
     float qreg[NQ];
 #pragma unroll
     for (int cc = 0; cc < D / 16; ++cc) {
-        const f32x4 t = load4<VEC>(Qh, qrow, seq_q, 16 * cc + 4 * lg, d);
+        const f32x4 t = widen<E>(load4r<E, VEC>(Qh, qrow, seq_q, 16 * cc + 4 * lg, d));
 #pragma unroll
         for (int i = 0; i < 4; ++i) qreg[4 * cc + i] = t[i];
     }
@@ -779,23 +833,26 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
     float m = FA_NEG_INF, l = 0.0f;
 
     // K rows kb + lr (A operand), V rows kb + 4lg + r (A operand of O^T).
-    auto load_k = [&](int kb, f32x4* kk) {
+    typedef typename RawOf<E>::type R;
+    auto load_k = [&](int kb, R* kk) {
 #pragma unroll
-        for (int cc = 0; cc < NKL; ++cc) kk[cc] = load4<VEC, true>(Kh, kb + lr, kend, 16 * cc + 4 * lg, d);
+        for (int cc = 0; cc < NKL; ++cc) kk[cc] = load4r<E, VEC, true>(Kh, kb + lr, kend, 16 * cc + 4 * lg, d);
     };
-    auto load_v = [&](int kb, f32x4* vv) {
+    auto load_v = [&](int kb, R* vv) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int hh = 0; hh < NVL; ++hh) {
                 if constexpr (VW == 4) {
-                    vv[r * NVL + hh] = load4<VEC, true>(Vh, kb + 4 * lg + r, kend, 64 * hh + 4 * lr, d);
+                    vv[r * NVL + hh] = load4r<E, VEC, true>(Vh, kb + 4 * lg + r, kend, 64 * hh + 4 * lr, d);
                 } else {
-                    // D = 32: 2 floats per lane (dv = 2*lr + j)
-                    f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
+                    // D = 32: 2 elements per lane (dv = 2*lr + j)
+                    R t;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) t[e] = E(0.0f);
                     const int key = kb + 4 * lg + r;
                     if (key < kend) {
-                        const float* vp = Vh + (size_t)key * d + VW * lr;
+                        const E* vp = Vh + (size_t)key * d + VW * lr;
 #pragma unroll
                         for (int e = 0; e < VW; ++e)
                             if (VW * lr + e < d) t[e] = vp[e];
@@ -807,20 +864,21 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
 
     // Scores of one 16-key block.  Blocked summation over d, 16 products
     // (4 MFMA steps) per block.
-    auto scores = [&](int kb, const f32x4* kk) -> f32x4 {
+    auto scores = [&](int kb, const R* kk) -> f32x4 {
         f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int cc = 0; cc < NKL; ++cc) {
             f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
+            const f32x4 kf = widen<E>(kk[cc]);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                t = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[cc][i], qreg[4 * cc + i], t, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[i], qreg[4 * cc + i], t, 0, 0, 0);
             s = (cc == 0) ? t : s + t;
         }
         return s;
     };
     // Masked online softmax + PV for one block (s[r] = score(key kb+4lg+r, qrow)).
-    auto finish = [&](int kb, f32x4 s, const f32x4* vv) {
+    auto finish = [&](int kb, f32x4 s, const R* vv) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int key = kb + 4 * lg + r;
@@ -845,15 +903,16 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int hh = 0; hh < NVL; ++hh)
+            for (int hh = 0; hh < NVL; ++hh) {
+                const f32x4 vf = widen<E>(vv[r * NVL + hh]);
 #pragma unroll
                 for (int j = 0; j < VW; ++j)
-                    o[hh * VW + j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[r * NVL + hh][j], s[r],
-                                                                         o[hh * VW + j], 0, 0, 0);
+                    o[hh * VW + j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[j], s[r], o[hh * VW + j], 0, 0, 0);
+            }
     };
 
     if constexpr (DBUF) {
-        f32x4 ka[NKL], va[4 * NVL], kb2[NKL], vb2[4 * NVL];
+        R ka[NKL], va[4 * NVL], kb2[NKL], vb2[4 * NVL];
         int kb = kbeg;
         if (kb < kend) {
             load_k(kb, ka);
@@ -875,7 +934,7 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
             kb += 16;
         }
     } else {
-        f32x4 kk[NKL], vv[4 * NVL];
+        R kk[NKL], vv[4 * NVL];
         if (kbeg < kend) {
             load_k(kbeg, kk);
             load_v(kbeg, vv);
@@ -1217,8 +1276,26 @@ FA_DECODE(64, 1, 4, 3)
 FA_DECODE(64, 0, 4, 3)
 FA_DECODE(128, 1, 3, 2)
 FA_DECODE(128, 0, 3, 2)
-FA_DECODE(256, 1, 2, 2)
-FA_DECODE(256, 0, 2, 2)
+FA_DECODE(256, 1, 1, 1)
+FA_DECODE(256, 0, 1, 1)
+
+// fa_decode_{bf16,f16}_d{D}_{VEC}: 16-bit Q/K/V widened to f32 as loaded.
+#define FA_DECODE_LP(D, TN, T, VEC, OCC1, OCC2)                                                   \
+    extern "C" __global__ void __launch_bounds__(256, FA_DECODE_DBUF ? OCC2 : OCC1)              \
+        fa_decode_##TN##_d##D##_##VEC(FaParams p) {                                              \
+        decode_body<D, VEC != 0, FA_DECODE_DBUF != 0, T>(p);                                     \
+    }
+#define FA_DECODE_LP_ALL(TN, T)              \
+    FA_DECODE_LP(32, TN, T, 1, 4, 4)         \
+    FA_DECODE_LP(32, TN, T, 0, 4, 4)         \
+    FA_DECODE_LP(64, TN, T, 1, 4, 3)         \
+    FA_DECODE_LP(64, TN, T, 0, 4, 3)         \
+    FA_DECODE_LP(128, TN, T, 1, 3, 2)        \
+    FA_DECODE_LP(128, TN, T, 0, 3, 2)        \
+    FA_DECODE_LP(256, TN, T, 1, 1, 1)        \
+    FA_DECODE_LP(256, TN, T, 0, 1, 1)
+FA_DECODE_LP_ALL(bf16, __bf16)
+FA_DECODE_LP_ALL(f16, _Float16)
 
 #define FA_MERGE(D) \
     extern "C" __global__ void __launch_bounds__(64) fa_merge_d##D(FaParams p) { merge_body<D>(p); }

@@ -271,10 +271,14 @@ def test_planning_16bit_inputs():
     assert describe(3, 1, 8, 16384, 16384, 128, True, dtype=fa.DTYPE_BF16).startswith("fa_prefill_lp_bf16_d128_2_t2")
     assert describe(2, 1, 2, 100, 100, 40, False, dtype=fa.DTYPE_F16).startswith("fa_prefill_lp_f16_d64_2_t1")
     assert describe(2, 1, 2, 100, 100, 20, False, dtype=fa.DTYPE_F16).startswith("fa_prefill_lp_f16_d32_0_t1")
-    assert "fa_decode" not in describe(3, 1, 32, 1, 32768, 128, False, dtype=fa.DTYPE_BF16)   # key split instead
-    assert "fa_merge_d128" in describe(3, 1, 32, 1, 32768, 128, False, dtype=fa.DTYPE_BF16)
+    s = describe(3, 1, 32, 1, 32768, 128, False, dtype=fa.DTYPE_BF16)   # AUTO: key-split 16-bit prefill
+    assert s.startswith("fa_prefill_lp_bf16_d128_2") and "fa_merge_d128 grid=32x1x1" in s
+    s = describe(3, 1, 32, 1, 32768, 128, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_BF16)   # split-KV, 16-bit loads
+    assert s.startswith("fa_decode_bf16_d128_1 grid=16x1x32") and "fa_merge_d128 grid=32x1x1" in s
+    assert describe(2, 1, 1, 4, 512, 64, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_F16).startswith("fa_decode_f16_d64_1")
+    assert describe(3, 1, 1, 4, 512, 62, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_F16).startswith("fa_decode_f16_d64_0")
     with pytest.raises(fa.FaError) as e:
-        describe(3, 1, 1, 4, 512, 64, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_BF16)
+        describe(1, 1, 1, 4, 512, 64, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_BF16)   # v1 never splits
     assert e.value.status == fa.FA_ERR_INVALID_ARG
     with pytest.raises(fa.FaError) as e:
         describe(3, 1, 1, 4, 512, 64, False, dtype=7)

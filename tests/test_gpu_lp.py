@@ -196,3 +196,30 @@ def test_lp_full_size_configs_against_naive_f64(dtype):
         print(f"[lp-naive-f64] {NAME[dtype]} {name}: max-abs {diff:.3g} (bound {tol:.3g}) rel-L2 {rl:.3g}",
               flush=True)
         assert diff <= tol and rl <= U[dtype], (name, diff, rl)
+
+
+@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16])
+def test_lp_split_kv_decode_is_exact_widening(dtype):
+    """The split-KV kernel (FA_PATH_SPLITKV) widens 16-bit loads to f32: no
+    probability rounding, so the f32 bar applies against the oracle on the
+    widened inputs.  AUTO takes the key-split 16-bit prefill (u bound)."""
+    from fa_testutil import assert_parity
+    rng = np.random.default_rng(40)
+    cases = [(32, 1, 4096, 128, False), (4, 16, 2048, 128, False), (2, 5, 1000, 64, True), (3, 40, 777, 32, False),
+             (1, 17, 3000, 256, False), (2, 1, 600, 60, False), (1, 33, 513, 37, True)]
+    for bh, sq, sk, d, causal in cases:
+        q16, q32 = to16(rng.standard_normal(bh * sq * d, dtype=np.float32), dtype)
+        k16, k32 = to16(rng.standard_normal(bh * sk * d, dtype=np.float32), dtype)
+        v16, v32 = to16(rng.standard_normal(bh * sk * d, dtype=np.float32), dtype)
+        want = oracle.run(2, q32, k32, v32, bh, sq, sk, d, causal, 64, 128)
+        for path, splits in ((fa.PATH_AUTO, 0), (fa.PATH_SPLITKV, 0), (fa.PATH_SPLITKV, 3)):
+            plan = fa.describe_launch(3, 1, bh, sq, sk, d, causal, path, splits, dtype)
+            what = f"{NAME[dtype]} decode {bh}x{sq}x{sk} d={d} causal={causal} path={path} splits={splits}"
+            print("[case]", what, plan, flush=True)
+            got = lp_device(dtype, q16, k16, v16, bh, sq, sk, d, causal, path, splits)
+            if "fa_decode" in plan:
+                assert_parity(got, want, what)
+            else:
+                assert_lp(got, want, v32, dtype, what)
+        got = lp_device(dtype, q16, k16, v16, bh, sq, sk, d, causal, fa.PATH_SPLITKV, 0, misalign=True)
+        assert_parity(got, want, f"{NAME[dtype]} decode misaligned {bh}x{sq}x{sk} d={d}")

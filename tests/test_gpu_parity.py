@@ -386,3 +386,43 @@ def test_long_context_config3_properties():
             for r in rows:
                 ref = oracle.naive_f64(q[sl_q], k[sl_q], v[sl_q], s, s, d, True, r, 1)
                 assert max_abs_diff(o[r], ref) < 2e-5, (variant, h, r)
+
+
+def test_host_slice_calls_from_many_threads():
+    """The crate's functions are Sync (concurrent calls legal); host-slice calls
+    from several threads give the same bits as the same calls made serially."""
+    import threading
+    shapes = [(2, 100, 130, 64, True), (1, 257, 257, 128, False), (3, 33, 500, 32, False), (1, 1000, 700, 96, True)]
+    inputs = []
+    for i, (bh, sq, sk, d, causal) in enumerate(shapes * 2):
+        inputs.append((bh, sq, sk, d, causal, random_vec(bh * sq * d, 10 + i), random_vec(bh * sk * d, 20 + i),
+                       random_vec(bh * sk * d, 30 + i)))
+    serial = []
+    for bh, sq, sk, d, causal, q, k, v in inputs:
+        out = np.zeros(bh * sq * d, np.float32)
+        fa.flash_attention_multihead_v3(q, k, v, 1, bh, sq, sk, d, fa.FlashAttentionConfig(causal=causal), out)
+        serial.append(out)
+    results = [None] * len(inputs)
+    errors = []
+
+    def work(i):
+        try:
+            bh, sq, sk, d, causal, q, k, v = inputs[i]
+            for _ in range(3):
+                out = np.zeros(bh * sq * d, np.float32)
+                fa.flash_attention_multihead_v3(q, k, v, 1, bh, sq, sk, d, fa.FlashAttentionConfig(causal=causal), out)
+                if results[i] is not None and not np.array_equal(results[i], out):
+                    errors.append(f"thread {i}: calls disagree")
+                results[i] = out
+        except Exception as e:   # pragma: no cover - reported below
+            errors.append(f"thread {i}: {e!r}")
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(len(inputs))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads), "a thread did not finish"
+    assert not errors, errors
+    for i, out in enumerate(results):
+        assert np.array_equal(out, serial[i]), i
