@@ -226,11 +226,21 @@ __device__ __forceinline__ void wait_vmcnt() {
 // max / sum over the 4 lanes (l%16 + 16k) that hold one query row.  Both
 // swaps hand every lane the pair in the same order, so all 4 lanes end
 // with bit-identical results.
+// max(a, b) as med3(a, b, +inf): one v_med3_f32, where fmaxf on values the
+// compiler cannot prove canonical (cross-lane moves, MFMA results) costs two
+// extra canonicalising v_max_f32.  The empty asm hides the constant so the
+// compiler cannot turn the med3 back into that max.  Differs from fmaxf
+// only for NaN inputs.
+__device__ __forceinline__ float fmax_fast(float a, float b) {
+    float inf = __builtin_huge_valf();
+    asm("" : "+s"(inf));
+    return __builtin_amdgcn_fmed3f(a, b, inf);
+}
 __device__ __forceinline__ float row4_max(float x) {
     auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const float y = fmax_fast(__uint_as_float(a[0]), __uint_as_float(a[1]));
     auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+    return fmax_fast(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float row4_sum(float x) {
     auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -307,6 +317,9 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     for (int j = 0; j < NOB; ++j) o[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
     float m = FA_NEG_INF;   // reference max of the row's log2-domain scores (same in its 4 lanes)
     float l = 0.0f;         // v2/v3: this lane's partial row sum; v1: full row sum
+    // -m (0 while m = -inf) as the QK^T chain's initial accumulator: the MFMA
+    // then yields S - m directly, with no per-score subtraction.
+    f32x4 nref = {0.0f, 0.0f, 0.0f, 0.0f};
 
     // Keys this workgroup visits: v1 visits every key (no causal skip,
     // src/v1.rs:209-216); v2/v3 stop after the block's last diagonal key
@@ -418,11 +431,13 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     const std::integral_constant<int, LDV> VL{};
 
     // ---- stage math ---------------------------------------------------------
-    // S^T for the stage's KB key blocks from `Ks`.  An MFMA chain rounds like
-    // a sequential FMA loop, and f32 VALU work does not overlap f32 MFMA on
-    // gfx950, so the summation order trades accuracy against VALU adds:
-    //  * D <= 128: two chains over alternate 16-column chunks of d (at most
-    //    64 products each), added once per stage;
+    // S^T - m for the stage's KB key blocks from `Ks` (each chain starts from
+    // nref = -m).  An MFMA chain rounds like a sequential FMA loop, and f32
+    // VALU work does not overlap f32 MFMA on gfx950 (an f32 MFMA holds the
+    // SIMD's VALU issue for its 32 cycles), so the summation order trades
+    // accuracy against VALU adds:
+    //  * D <= 128: one chain over d per key block (N(0,1)-scale logits keep
+    //    its rounding far inside the f32 parity bar);
     //  * D = 256: each 128-bit K read feeds a fresh 4-step (16-product) chain
     //    that is added to the running sum -- blocks of 16 bring the error down
     //    to that of the crate's 16-lane AVX-512 dot products
@@ -446,18 +461,18 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             for (int cc = 0; cc < PRE && cc < NC; ++cc) k_chunk(Ks, cc, kpre[cc]);
         }
     };
-    auto qk_mfma = [&](const f32x4* kk, int cc, f32x4* s, f32x4* s2) {
+    auto qk_mfma = [&](const f32x4* kk, int cc, f32x4* s) {
 #pragma unroll
         for (int b = 0; b < KB; ++b) {
             if constexpr (BLOCKED_QK) {
-                f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
+                f32x4 t = (cc == 0) ? nref : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     t = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[b][i], qreg[4 * cc + i], t, 0, 0, 0);
                 s[b] = (cc == 0) ? t : s[b] + t;
             } else {
-                f32x4& acc = (cc & 1) ? s2[b] : s[b];
-                if (cc < 2) acc = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+                f32x4& acc = s[b];
+                if (cc == 0) acc = nref;
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[b][i], qreg[4 * cc + i], acc, 0, 0, 0);
@@ -465,7 +480,6 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         }
     };
     auto qk_stage = [&](const float* Ks, f32x4* s) {   // after qk_preload(Ks)
-        f32x4 s2[BLOCKED_QK ? 1 : KB];   // second chain (odd chunks)
         if constexpr (PRE > 0) {
             constexpr int KR = PRE + 1;
             f32x4 kk[KR][KB];
@@ -475,7 +489,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
                 for (int b = 0; b < KB; ++b) kk[cc][b] = kpre[cc][b];
 #pragma unroll
             for (int cc = 0; cc < NC; ++cc) {
-                qk_mfma(kk[cc % KR], cc, s, s2);
+                qk_mfma(kk[cc % KR], cc, s);
                 if (cc + PRE < NC) k_chunk(Ks, cc + PRE, kk[(cc + PRE) % KR]);
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -487,14 +501,8 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
 #pragma unroll
             for (int cc = 0; cc < NC; ++cc) {
                 if (cc + 1 < NC) k_chunk(Ks, cc + 1, kk[(cc + 1) & 1]);
-                qk_mfma(kk[cc & 1], cc, s, s2);
+                qk_mfma(kk[cc & 1], cc, s);
                 __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-        if constexpr (!BLOCKED_QK) {
-            if constexpr (NC > 1) {
-#pragma unroll
-                for (int b = 0; b < KB; ++b) s[b] += s2[b];
             }
         }
     };
@@ -539,47 +547,56 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     // normalise / un-normalise round trip, src/v1.rs:291-385).  After
     // pv_preload(Vs).
     auto softmax_pv = [&](f32x4* s, const float* Vs) {
-        float mt = s[0][0];
+        // s holds S - m (S itself while m = -inf: nref was 0).
+        float mt = fmax_fast(s[0][0], s[0][1]);
 #pragma unroll
         for (int b = 0; b < KB; ++b)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) mt = fmaxf(mt, s[b][r]);
+            for (int r = (b == 0) ? 2 : 0; r < 4; ++r) mt = fmaxf(mt, s[b][r]);
         mt = row4_max(mt);
         // Lazy reference max: it moves only when the stage max exceeds it by
         // more than kLazyMax (log2 units), so exponentials stay <= 2^kLazyMax
-        // and rescaling the accumulators is rare; otherwise corr is exactly 1.
+        // and rescaling the accumulators is rare; otherwise nothing changes.
         // The final O / l is the same quotient (each term and l share the
         // reference), to f32 rounding.
-        const bool grow = mt > m + kLazyMax;   // from m = -inf: any visible key
-        const float m_new = grow ? mt : m;
-        const float m_use = (m_new == FA_NEG_INF) ? 0.0f : m_new;
-        float ps = 0.0f;
+        const bool seen = m != FA_NEG_INF;
+        const bool grow = mt > (seen ? kLazyMax : FA_NEG_INF);   // from m = -inf: any visible key
+        const float delta = grow ? mt : 0.0f;                    // the reference moves up by delta
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+            for (int b = 0; b < KB; ++b) s[b] -= delta;
+            if (grow) m = (seen ? m : 0.0f) + delta;
+            const float nm = (m == FA_NEG_INF) ? 0.0f : -m;
+            nref = (f32x4){nm, nm, nm, nm};
+        }
 #pragma unroll
         for (int b = 0; b < KB; ++b)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                s[b][r] = fa_exp2(s[b][r] - m_use);
-                ps += s[b][r];
-            }
-        // m = -inf: nothing accumulated yet (o and l are 0), factor 0
-        const float corr = (m == FA_NEG_INF) ? 0.0f : fa_exp2(m - m_new);
-        const bool rescale = grow && m != FA_NEG_INF;
-        m = m_new;
+            for (int r = 0; r < 4; ++r) s[b][r] = fa_exp2(s[b][r]);
+        float ps = s[0][0];
+#pragma unroll
+        for (int b = 0; b < KB; ++b)
+#pragma unroll
+            for (int r = (b == 0) ? 1 : 0; r < 4; ++r) ps += s[b][r];
+        // A row seen before whose reference moved scales o and l by
+        // 2^-delta; a row with none before has o = l = 0 (no factor needed).
+        const bool rescale = grow && seen;
         if (VARIANT == 1) {
+            const float corr = rescale ? fa_exp2(-delta) : 1.0f;
             const float l_new = corr * l + row4_sum(ps);
             const float f = l * corr;
 #pragma unroll
             for (int j = 0; j < NOB; ++j) o[j] *= f;
             l = l_new;
         } else {
-            l = corr * l + ps;
-            // corr is exactly 1 for a row whose reference did not move (and
-            // o is still 0 for a row that had none); skip the rescale when
-            // that holds for every row of the wave.
+            // skipped unless some row of the wave rescales
             if (__builtin_amdgcn_ballot_w64(rescale) != 0) {
+                const float corr = rescale ? fa_exp2(-delta) : 1.0f;
+                l *= corr;
 #pragma unroll
                 for (int j = 0; j < NOB; ++j) o[j] *= corr;
             }
+            l += ps;
         }
         // O^T += V^T P^T: 4 keys per MFMA step (key 16b + 4g + r in lane group
         // g), a scheduling barrier per step.
@@ -637,13 +654,12 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         // is issued right after stage st's softmax + PV, and one barrier
         // closes the step.  The loop is unrolled by two so every buffer is a
         // compile-time choice.
-        if (nst > 0) {
-            fill_stage(KL, Kh, k0, Kb0);
-            fill_stage(VL, Vh, k0, Vb0);
-        }
-        if (nst > 1) fill_stage(KL, Kh, k0 + SK, Kb1);
+        // Q and K(0) first; V(0) and K(1) stream in under stage 0's QK^T.
+        if (nst > 0) fill_stage(KL, Kh, k0, Kb0);
         wait_vmcnt<0>();
         __syncthreads();
+        if (nst > 0) fill_stage(VL, Vh, k0, Vb0);
+        if (nst > 1) fill_stage(KL, Kh, k0 + SK, Kb1);
         f32x4 s_cur[KB];
         bool act_cur = nst > 0 && stage_active(0);
         if (act_cur) {
@@ -651,7 +667,8 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             qk_stage(Kb0, s_cur);
             mask_stage(s_cur, k0);
         }
-        __syncthreads();   // Kb0 free for K(2)
+        wait_vmcnt<0>();
+        __syncthreads();   // V(0), K(1) resident; Kb0 free for K(2)
         auto step = [&](auto parity, int st) {
             constexpr int P = decltype(parity)::value;
             float* k_fill = P ? Kb1 : Kb0;        // K(st+2) -> buffer of K(st)
