@@ -274,6 +274,15 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
             }
             if (per > 0 && (max_st + per - 1) / per < 2) per = 0;
             if (per > 0 && (bh * sq > imax || per * SKs > imax)) return FA_ERR_UNSUPPORTED;
+            // f32 v3 with 128-bit DMA and d = D = 128: pair query blocks nqb-1-r
+            // and r in one workgroup (equal causal work per workgroup; the
+            // second block's loads overlap the first's last step) when the
+            // pairs fill whole rounds of one workgroup per CU.
+            if (per == 0 && !lp && variant == 3 && vec && (size_t)D == d && D == 128 && nqb % 2 == 0 &&
+                (nqb / 2 * bh) % (size_t)num_cus == 0) {
+                p.two_blocks = 1;
+                plan->first.gx = static_cast<unsigned>(nqb / 2 * bh);
+            }
             if (per > 0) {
                 const size_t nks = (max_st + per - 1) / per;
                 if (nks > 65535 || nks > (size_t)kMaxSplits) return FA_ERR_UNSUPPORTED;
@@ -747,6 +756,7 @@ int fa_describe_launch(int variant, size_t batch, size_t heads, size_t sq, size_
             std::snprintf(tmp, sizeof(tmp), "%s grid=%ux%ux%u block=%u", plan.first.name.c_str(), plan.first.gx,
                           plan.first.gy, plan.first.gz, plan.first.bx);
             text = tmp;
+            if (plan.p.two_blocks) text += " two_blocks";
             if (plan.split) {
                 std::snprintf(tmp, sizeof(tmp), "; %s grid=%ux%ux%u block=%u; splits=%d", plan.second.name.c_str(),
                               plan.second.gx, plan.second.gy, plan.second.gz, plan.second.bx, plan.p.num_splits);

@@ -161,6 +161,25 @@ __device__ __forceinline__ void map_block(const FaParams& p, int x, int& qb, int
     qb = p.causal ? (p.nqb - 1 - rank) : rank;
 }
 
+// Two-block grid (bh * nqb / 2 workgroups, nqb even): workgroup x takes
+// query blocks nqb-1-r and r of one (batch, head), with the (bh, r) order of
+// map_block over nqb / 2 ranks.  Causal blocks r and nqb-1-r together cover
+// nqb + 1 stage pairs, the same for every workgroup.
+__device__ __forceinline__ void map_pair(const FaParams& p, int x, int& qa, int& qb2, int& bh) {
+    int rank;
+    if (p.bh % 8 == 0) {
+        const int hpx = p.bh / 8;
+        const int xcd = x % 8, s = x / 8;
+        bh = (s % hpx) * 8 + xcd;
+        rank = s / hpx;
+    } else {
+        bh = x % p.bh;
+        rank = x / p.bh;
+    }
+    qa = p.nqb - 1 - rank;
+    qb2 = rank;
+}
+
 // Key-split grid: a compact 1-D list of the workgroups that have keys to
 // process (a grid padded with idle workgroups lets the dispatcher queue
 // working ones behind busy CUs).  Row y holds split y of every query block
@@ -286,11 +305,16 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     const int li = lane & 15;
 
     const bool splitk = p.part_o != nullptr;
-    int qb, bh, ysplit = 0;
+    // two_blocks (v3, no key split): this workgroup runs query blocks
+    // nqb-1-r and then r of one (batch, head) -- equal causal work per
+    // workgroup, and the second block's loads overlap the first's last step.
+    const bool pairs = VARIANT == 3 && D == 128 && !splitk && p.two_blocks != 0;
+    int qb, bh, ysplit = 0, qb_second = 0;
     if (splitk) map_block_split(p, qb, bh, ysplit);
+    else if (pairs) map_pair(p, blockIdx.x, qb, qb_second, bh);
     else map_block(p, blockIdx.x, qb, bh);
     const int seq_q = p.seq_q, seq_k = p.seq_k, d = p.d;
-    const int q0 = qb * BQ;
+    int q0 = qb * BQ;
     const float* __restrict__ Qh = p.q + (size_t)bh * seq_q * d;
     const float* __restrict__ Kh = p.k + (size_t)bh * seq_k * d;
     const float* __restrict__ Vh = p.v + (size_t)bh * seq_k * d;
@@ -302,15 +326,23 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     // pre-multiplied by scale * log2(e) so scores come out of the MFMA in the
     // exp2 domain (src/v2.rs:171-173 multiplies after the dot; the product
     // differs by one f32 rounding per element of Q).
-    const int row_first = q0 + 16 * wave;
-    const int qrow = row_first + li;
+    int row_first = q0 + 16 * wave;
+    int qrow = row_first + li;
     float qreg[NQ];
+    auto load_q = [&](int row) {   // unscaled
 #pragma unroll
-    for (int cc = 0; cc < NC; ++cc) {
-        const f32x4 t = load4<LOADER != 0>(Qh, qrow, seq_q, 16 * cc + 4 * g, d);
+        for (int cc = 0; cc < NC; ++cc) {
+            const f32x4 t = load4<LOADER != 0>(Qh, row, seq_q, 16 * cc + 4 * g, d);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) qreg[4 * cc + i] = t[i] * c;
-    }
+            for (int i = 0; i < 4; ++i) qreg[4 * cc + i] = t[i];
+        }
+    };
+    auto scale_q = [&]() {
+#pragma unroll
+        for (int i = 0; i < NQ; ++i) qreg[i] *= c;
+    };
+    load_q(qrow);
+    scale_q();
 
     f32x4 o[NOB];
 #pragma unroll
@@ -324,8 +356,8 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     // Keys this workgroup visits: v1 visits every key (no causal skip,
     // src/v1.rs:209-216); v2/v3 stop after the block's last diagonal key
     // (src/v2.rs:208-212, src/v3.rs:396-410).
-    int kend = seq_k;
-    if (VARIANT != 1 && causal) kend = min(seq_k, q0 + BQ);
+    auto block_end = [&](int q0_) { return (VARIANT != 1 && causal) ? min(seq_k, q0_ + BQ) : seq_k; };
+    int kend = block_end(q0);
     // Key split (v2/v3 on grids smaller than the GPU): the workgroup for
     // split y takes the split_len keys from y * split_len of its block's
     // range and writes a partial (m, l, O) that fa_merge combines.
@@ -387,6 +419,10 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         if (kbase + SK <= seq_k) {
             const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<float*>(src + (size_t)kbase * d), (short)0, SK * d * 4, 0x00020000);
+            // LDS destinations from one opaque per-stage base: the compiler
+            // would otherwise keep every run's address in its own SGPR.
+            int w256 = wave * 256;
+            asm volatile("" : "+s"(w256));
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
                 const int run = i * NW + wave;
@@ -394,7 +430,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
                 // only the image's last run can have lanes past it
                 if (((i + 1) * NW <= RUNS || run < RUNS) && (TOTAL % 64 == 0 || run < RUNS - 1 || voff[i] >= 0))
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                        rs, (__attribute__((address_space(3))) void*)(dst + run * 256), 16, voff[i], 0, 0, 0);
+                        rs, (__attribute__((address_space(3))) void*)(dst + i * NW * 256 + w256), 16, voff[i], 0, 0, 0);
             }
         } else {
 #pragma unroll
@@ -646,6 +682,39 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         return true;
     };
 
+    // Final normalisation with the l > 0 guard (src/v2.rs:375-382; v1's
+    // accumulator is already normalised, src/v1.rs:389-393).
+    auto write_out = [&]() {
+        float inv = 1.0f;
+        if (VARIANT != 1) {
+            const float lt = row4_sum(l);
+            inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        }
+        if (qrow < seq_q) {
+            float* orow = Oh + (size_t)qrow * d;
+#pragma unroll
+            for (int hh = 0; hh < NVR; ++hh)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int dv0 = 64 * hh + VW * (4 * g + r);
+                    if (LOADER != 0 && dv0 + VW <= d) {
+                        if constexpr (VW == 4) {
+                            const f32x4 t = {o[4 * hh][r] * inv, o[4 * hh + 1][r] * inv, o[4 * hh + 2][r] * inv,
+                                             o[4 * hh + 3][r] * inv};
+                            *reinterpret_cast<f32x4*>(orow + dv0) = t;
+                        } else {
+                            const f32x2 t = {o[0][r] * inv, o[1][r] * inv};
+                            *reinterpret_cast<f32x2*>(orow + dv0) = t;
+                        }
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < VW; ++j)
+                            if (dv0 + j < d) orow[dv0 + j] = o[VW * hh + j][r] * inv;
+                    }
+                }
+        }
+    };
+
     if constexpr (VARIANT == 3) {
         // Double-buffered K and V (src/v3.rs:445-483: the next tile's scores
         // are issued before the current tile is finished).  At step st, K(st+2)
@@ -654,48 +723,98 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         // is issued right after stage st's softmax + PV, and one barrier
         // closes the step.  The loop is unrolled by two so every buffer is a
         // compile-time choice.
+        // With two blocks the stages of both run as one sequence g = 0 ..
+        // nA + nB - 1 (block A: stages 0 .. nA-1), so the K/V loads of
+        // block B's first stages are issued during block A's last steps like
+        // any other; block B's Q is loaded at the start of A's last step (Q is
+        // idle there) and the switch happens between that step's PV and the
+        // QK^T of B's first stage.
+        const int nA = nst;
+        const int q0_b = qb_second * BQ;
+        const int nB = pairs ? (block_end(q0_b) + SK - 1) / SK : 0;
+        const int ntot = nA + nB;
+        auto kb_of = [&](int gs) { return gs < nA ? k0 + gs * SK : (gs - nA) * SK; };
+        auto gstage_active = [&](int gs) -> bool {
+            const int kbase = kb_of(gs);
+            const int rf = (gs < nA ? qb * BQ : q0_b) + 16 * wave;
+            return kbase < seq_k && !(causal && kbase > rf + 15);
+        };
         // Q and K(0) first; V(0) and K(1) stream in under stage 0's QK^T.
-        if (nst > 0) fill_stage(KL, Kh, k0, Kb0);
+        if (ntot > 0) fill_stage(KL, Kh, kb_of(0), Kb0);
         wait_vmcnt<0>();
         __syncthreads();
-        if (nst > 0) fill_stage(VL, Vh, k0, Vb0);
-        if (nst > 1) fill_stage(KL, Kh, k0 + SK, Kb1);
+        if (ntot > 0) fill_stage(VL, Vh, kb_of(0), Vb0);
+        if (ntot > 1) fill_stage(KL, Kh, kb_of(1), Kb1);
         f32x4 s_cur[KB];
-        bool act_cur = nst > 0 && stage_active(0);
+        bool act_cur = ntot > 0 && gstage_active(0);
         if (act_cur) {
             qk_preload(Kb0);
             qk_stage(Kb0, s_cur);
-            mask_stage(s_cur, k0);
+            mask_stage(s_cur, kb_of(0));
         }
         wait_vmcnt<0>();
         __syncthreads();   // V(0), K(1) resident; Kb0 free for K(2)
-        auto step = [&](auto parity, int st) {
+        auto step = [&](auto parity, int gs) {
             constexpr int P = decltype(parity)::value;
-            float* k_fill = P ? Kb1 : Kb0;        // K(st+2) -> buffer of K(st)
-            float* v_fill = P ? Vb0 : Vb1;        // V(st+1)
-            const float* k_next = P ? Kb0 : Kb1;  // K(st+1)
-            const float* v_cur = P ? Vb1 : Vb0;   // V(st)
-            const bool has_next = st + 1 < nst;
-            if (st + 2 < nst) fill_stage(KL, Kh, k0 + (st + 2) * SK, k_fill);
-            if (has_next) fill_stage(VL, Vh, k0 + (st + 1) * SK, v_fill);
-            const bool act_nxt = has_next && stage_active(st + 1);
+            float* k_fill = P ? Kb1 : Kb0;        // K(gs+2) -> buffer of K(gs)
+            float* v_fill = P ? Vb0 : Vb1;        // V(gs+1)
+            const float* k_next = P ? Kb0 : Kb1;  // K(gs+1)
+            const float* v_cur = P ? Vb1 : Vb0;   // V(gs)
+            const bool has_next = gs + 1 < ntot;
+            if (gs + 2 < ntot) fill_stage(KL, Kh, kb_of(gs + 2), k_fill);
+            if (has_next) fill_stage(VL, Vh, kb_of(gs + 1), v_fill);
+            const bool switch_now = pairs && gs == nA - 1 && nB > 0;
+            if (switch_now) load_q(q0_b + 16 * wave + li);
+            const bool act_nxt = has_next && gstage_active(gs + 1);
             // This stage's softmax + PV, then the next stage's QK^T from the
             // other buffer, with no barrier between them.  Both stages are
             // resident: their first operands are read before the softmax.
             if (act_cur) pv_preload(v_cur);
             if (act_nxt) qk_preload(k_next);
             if (act_cur) softmax_pv(s_cur, v_cur);
+            if (switch_now) {
+                // block A's rows, full 128-bit stores (two_blocks needs d = D)
+                const float lt = row4_sum(l);
+                const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+                if (qrow < seq_q) {
+                    float* orow = Oh + (size_t)qrow * D;
+#pragma unroll
+                    for (int hh = 0; hh < NVR; ++hh)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            if constexpr (VW == 4) {
+                                const f32x4 t = {o[4 * hh][r] * inv, o[4 * hh + 1][r] * inv,
+                                                 o[4 * hh + 2][r] * inv, o[4 * hh + 3][r] * inv};
+                                *reinterpret_cast<f32x4*>(orow + 64 * hh + VW * (4 * g + r)) = t;
+                            } else {
+                                const f32x2 t = {o[0][r] * inv, o[1][r] * inv};
+                                *reinterpret_cast<f32x2*>(orow + VW * (4 * g + r)) = t;
+                            }
+                        }
+                }
+                q0 = q0_b;
+                row_first = q0 + 16 * wave;
+                qrow = row_first + li;
+#pragma unroll
+                for (int j = 0; j < NOB; ++j) o[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+                m = FA_NEG_INF;
+                l = 0.0f;
+                nref = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+                scale_q();
+            }
             if (act_nxt) {
                 qk_stage(k_next, s_cur);
-                mask_stage(s_cur, k0 + (st + 1) * SK);
+                mask_stage(s_cur, kb_of(gs + 1));
             }
-            wait_vmcnt<0>();
-            __syncthreads();
+            if (has_next) {
+                wait_vmcnt<0>();
+                __syncthreads();
+            }
             act_cur = act_nxt;
         };
-        for (int st = 0; st < nst; st += 2) {
-            step(std::integral_constant<int, 0>{}, st);
-            if (st + 1 < nst) step(std::integral_constant<int, 1>{}, st + 1);
+        for (int gs = 0; gs < ntot; gs += 2) {
+            step(std::integral_constant<int, 0>{}, gs);
+            if (gs + 1 < ntot) step(std::integral_constant<int, 1>{}, gs + 1);
         }
     } else {
         // Single LDS stage; the next stage's global loads are issued into
@@ -749,36 +868,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         return;
     }
 
-    // Final normalisation with the l > 0 guard (src/v2.rs:375-382; v1's
-    // accumulator is already normalised, src/v1.rs:389-393).
-    float inv = 1.0f;
-    if (VARIANT != 1) {
-        const float lt = row4_sum(l);
-        inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-    }
-    if (qrow < seq_q) {
-        float* orow = Oh + (size_t)qrow * d;
-#pragma unroll
-        for (int hh = 0; hh < NVR; ++hh)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int dv0 = 64 * hh + VW * (4 * g + r);
-                if (LOADER != 0 && dv0 + VW <= d) {
-                    if constexpr (VW == 4) {
-                        const f32x4 t = {o[4 * hh][r] * inv, o[4 * hh + 1][r] * inv, o[4 * hh + 2][r] * inv,
-                                         o[4 * hh + 3][r] * inv};
-                        *reinterpret_cast<f32x4*>(orow + dv0) = t;
-                    } else {
-                        const f32x2 t = {o[0][r] * inv, o[1][r] * inv};
-                        *reinterpret_cast<f32x2*>(orow + dv0) = t;
-                    }
-                } else {
-#pragma unroll
-                    for (int j = 0; j < VW; ++j)
-                        if (dv0 + j < d) orow[dv0 + j] = o[VW * hh + j][r] * inv;
-                }
-            }
-    }
+    write_out();
 }
 
 // ---------------------------------------------------------------------------

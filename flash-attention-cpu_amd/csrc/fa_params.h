@@ -30,6 +30,8 @@ typedef struct FaParams {
     int pair_w;          // prefill, two workgroups per CU: causal ranks per dispatch round
                          // (odd rounds run in reverse so each CU pairs a long and a short
                          // block); 0 = plain longest-first order
+    int two_blocks;      // f32 v3 prefill, d_head 128: each workgroup runs query blocks
+                         // nqb-1-r and r of one (batch, head); nqb even, grid = bh * nqb / 2
 } FaParams;
 
 

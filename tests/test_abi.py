@@ -179,7 +179,12 @@ def describe(variant, b, h, sq, sk, d, causal, path=fa.PATH_AUTO, splits=0, dtyp
 
 
 def test_planning_prefill_kernels():
-    assert describe(3, 1, 32, 2048, 2048, 128, True).startswith("fa_prefill_v3_d128_2 grid=512x1x1 block=512")
+    # v3 pairs query blocks nqb-1-r and r when the pairs fill whole rounds (256 CUs)
+    assert describe(3, 1, 32, 2048, 2048, 128, True) == "fa_prefill_v3_d128_2 grid=256x1x1 block=512 two_blocks"
+    assert describe(3, 1, 8, 16384, 16384, 128, True).endswith("grid=512x1x1 block=512 two_blocks")
+    assert describe(3, 1, 16, 2048, 2048, 128, True) == "fa_prefill_v3_d128_2 grid=256x1x1 block=512"   # 128 pairs
+    assert describe(3, 1, 32, 2048, 2048, 120, True) == "fa_prefill_v3_d128_2 grid=512x1x1 block=512"   # d < D
+    assert describe(3, 1, 32, 1920, 2048, 128, True) == "fa_prefill_v3_d128_2 grid=480x1x1 block=512"   # nqb odd
     assert describe(2, 1, 32, 2048, 2048, 128, True).startswith("fa_prefill_v2_d128_1 grid=512x1x1")
     assert describe(1, 1, 32, 2048, 2048, 128, True).startswith("fa_prefill_v1_d128_1")
     assert describe(2, 1, 8, 16384, 16384, 128, True).startswith("fa_prefill_v2_d128_1 grid=1024x1x1")

@@ -344,6 +344,32 @@ def test_key_split_prefill_matches_oracle():
             assert_parity(a, want, f"auto v{variant} {bh},{sq},{sk},{d},{causal}")
 
 
+def test_two_block_workgroups_match_oracle():
+    """f32 v3 grids whose block pairs fill whole rounds of the GPU run query
+    blocks nqb-1-r and r in one workgroup, the second block's loads issued
+    during the first's last step.  Ragged last blocks, non-causal, and key
+    ranges that end inside a stage; v2 (one block per workgroup) agrees."""
+    rng = np.random.default_rng(91)
+    num_cus = 256   # MI355X; the pairing needs (nqb / 2) * bh to be a multiple of it
+    for sq, sk, d, causal in [(200, 300, 128, True), (256, 256, 128, False), (250, 190, 128, False),
+                              (130, 1000, 128, True)]:
+        bh = num_cus   # nqb = 2: one pair per (batch, head)
+        q = rng.standard_normal(bh * sq * d, dtype=np.float32)
+        k = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        v = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        tag = f"two-block {bh},{sq},{sk},{d},{causal}"
+        print("[case]", tag, flush=True)
+        assert "two_blocks" in fa.describe_launch(3, 1, bh, sq, sk, d, causal), tag
+        assert "two_blocks" not in fa.describe_launch(2, 1, bh, sq, sk, d, causal)
+        want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+        got = _device_run(3, q, k, v, bh, sq, sk, d, causal, guard=64)
+        assert_parity(got, want, tag)
+        assert max_abs_diff(got, _device_run(2, q, k, v, bh, sq, sk, d, causal, guard=64)) < 2e-5, tag
+    # padded d_head (d < D) and d_head < 128 keep one block per workgroup
+    assert "two_blocks" not in fa.describe_launch(3, 1, 256, 200, 300, 100, True)
+    assert "two_blocks" not in fa.describe_launch(3, 1, 256, 200, 300, 64, True)
+
+
 def test_device_api_bounds_and_determinism():
     for bh, sq, sk, d, causal in [(3, 130, 77, 128, True), (2, 257, 300, 64, False), (1, 129, 129, 256, True),
                                   (2, 100, 50, 20, False), (5, 3, 1000, 128, False)]:
