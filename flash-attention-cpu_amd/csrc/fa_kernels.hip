@@ -589,16 +589,21 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         for (int b = 0; b < KB; ++b)
 #pragma unroll
             for (int r = (b == 0) ? 2 : 0; r < 4; ++r) mt = fmaxf(mt, s[b][r]);
-        mt = row4_max(mt);
         // Lazy reference max: it moves only when the stage max exceeds it by
         // more than kLazyMax (log2 units), so exponentials stay <= 2^kLazyMax
         // and rescaling the accumulators is rare; otherwise nothing changes.
         // The final O / l is the same quotient (each term and l share the
-        // reference), to f32 rounding.
+        // reference), to f32 rounding.  The row's maximum (a reduction over
+        // its 4 lanes) is needed only when some lane's own maximum passes the
+        // threshold.
         const bool seen = m != FA_NEG_INF;
-        const bool grow = mt > (seen ? kLazyMax : FA_NEG_INF);   // from m = -inf: any visible key
-        const float delta = grow ? mt : 0.0f;                    // the reference moves up by delta
-        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        const float thr = seen ? kLazyMax : FA_NEG_INF;   // from m = -inf: any visible key
+        bool grow = false;
+        float delta = 0.0f;                                // the reference moves up by delta
+        if (__builtin_amdgcn_ballot_w64(mt > thr) != 0) {
+            mt = row4_max(mt);
+            grow = mt > thr;
+            delta = grow ? mt : 0.0f;
 #pragma unroll
             for (int b = 0; b < KB; ++b) s[b] -= delta;
             if (grow) m = (seen ? m : 0.0f) + delta;
