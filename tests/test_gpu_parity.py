@@ -370,6 +370,29 @@ def test_two_block_workgroups_match_oracle():
     assert "two_blocks" not in fa.describe_launch(3, 1, 256, 200, 300, 64, True)
 
 
+def test_reference_moves_mid_sequence():
+    """Keys 0..63 with tiny logits (std 0.05) and later keys with large ones
+    (std 2.4): a row's maximum jumps past the lazy 2^8 threshold after the
+    first 64-key stage (checked on the CPU for 30-98 % of the rows), so the
+    reference moves mid-sequence and the O / l rescale and the -m starting
+    accumulator run there, including on the two-block grid (first rows of
+    this list)."""
+    rng = np.random.default_rng(5)
+    for bh, sq, sk, d, causal, variant in [(256, 256, 256, 128, True, 3), (256, 256, 256, 128, False, 3),
+                                           (4, 300, 700, 128, True, 2), (4, 300, 700, 64, False, 3),
+                                           (2, 200, 640, 256, False, 3)]:
+        q = rng.standard_normal((bh, sq, d), dtype=np.float32)
+        ramp = np.where(np.arange(sk) < 64, 0.05, 2.4).astype(np.float32)[None, :, None]
+        k = (rng.standard_normal((bh, sk, d), dtype=np.float32) * ramp).astype(np.float32)
+        v = rng.standard_normal((bh, sk, d), dtype=np.float32)
+        q, k, v = q.ravel(), k.ravel(), v.ravel()
+        tag = f"rising v{variant} {bh},{sq},{sk},{d},{causal}"
+        print("[case]", tag, flush=True)
+        want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+        got = _device_run(variant, q, k, v, bh, sq, sk, d, causal, guard=64)
+        assert_parity(got, want, tag)
+
+
 def test_device_api_bounds_and_determinism():
     for bh, sq, sk, d, causal in [(3, 130, 77, 128, True), (2, 257, 300, 64, False), (1, 129, 129, 256, True),
                                   (2, 100, 50, 20, False), (5, 3, 1000, 128, False)]:
