@@ -35,6 +35,7 @@ constexpr int kMaxDevices = 64;
 constexpr int kMaxD = 256;
 constexpr int kDecodeRows = 16;     // query rows per split-KV wave
 constexpr int kDecodeWaves = 4;     // waves per split-KV workgroup
+constexpr int kRowsMaxQ = 4;        // row-streaming decode: most query rows
 
 struct DeviceState {
     std::once_flag once;
@@ -152,8 +153,8 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     const int dtype = opts ? opts->dtype : FA_DTYPE_F32;
     if (dtype != FA_DTYPE_F32 && dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F16) return FA_ERR_INVALID_ARG;
     const bool lp = dtype != FA_DTYPE_F32;   // 16-bit inputs: the fa_prefill_lp kernels
-    if (path < FA_PATH_AUTO || path > FA_PATH_SPLITKV) return FA_ERR_INVALID_ARG;
-    if (path == FA_PATH_SPLITKV && variant == 1) return FA_ERR_INVALID_ARG;
+    if (path < FA_PATH_AUTO || path > FA_PATH_SPLITKV_ROWS) return FA_ERR_INVALID_ARG;
+    if ((path == FA_PATH_SPLITKV || path == FA_PATH_SPLITKV_ROWS) && variant == 1) return FA_ERR_INVALID_ARG;
     if (opts && opts->num_splits < 0) return FA_ERR_INVALID_ARG;
     if (d > (size_t)kMaxD) return FA_ERR_UNSUPPORTED;
     const size_t imax = 0x7fffffff;
@@ -180,9 +181,12 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     const size_t rows = (size_t)(lp ? fa_lp_rows() : fa_prefill_rows(D));   // query rows per prefill workgroup
     const size_t nqb = (sq + rows - 1) / rows;
     const size_t nqt = (sq + kDecodeRows - 1) / kDecodeRows;
+    // Row-streaming decode: seq_q <= 4, f32, 128-bit loads.
+    const bool rows_ok = !lp && vec && sq <= (size_t)kRowsMaxQ;
+    if (path == FA_PATH_SPLITKV_ROWS && !rows_ok) return FA_ERR_UNSUPPORTED;
     bool split = false;
     if (variant != 1) {
-        if (path == FA_PATH_SPLITKV) {
+        if (path == FA_PATH_SPLITKV || path == FA_PATH_SPLITKV_ROWS) {
             split = true;
         } else if (path == FA_PATH_AUTO && !lp) {
             // (16-bit inputs: the key-split 16-bit prefill is faster than the
@@ -191,8 +195,9 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
             split = sq <= 64 && sk >= 512 && nqb * bh < (size_t)num_cus;
         }
     }
+    const bool row_decode = split && rows_ok && (path == FA_PATH_SPLITKV_ROWS || path == FA_PATH_AUTO);
     if (split && nqt * bh > 65535) {
-        if (path == FA_PATH_SPLITKV) return FA_ERR_UNSUPPORTED;
+        if (path == FA_PATH_SPLITKV || path == FA_PATH_SPLITKV_ROWS) return FA_ERR_UNSUPPORTED;
         split = false;
     }
     plan->split = split;
@@ -314,8 +319,9 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
         nsplit = (size_t)opts->num_splits;
     } else {
         // resident decode workgroups per CU at the kernel's register use
-        // (D = 256: one, with 424 of 512 registers per lane)
-        const size_t wg_per_cu = D <= 128 ? 2 : 1;
+        // (D = 256: one, with 424 of 512 registers per lane; the
+        // row-streaming kernel: two)
+        const size_t wg_per_cu = (row_decode || D <= 128) ? 2 : 1;
         const size_t slots = wg_per_cu * (size_t)num_cus;
         nsplit = slots / (nqt * bh);
         if (nsplit < 1) nsplit = 1;
@@ -329,7 +335,10 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     p.num_splits = static_cast<int>(nsplit);
     p.split_len = static_cast<int>(split_len);
     p.merge_scale = p.scale_log2e;   // decode partial maxima are raw scores
-    if (lp) {
+    if (row_decode) {
+        const int rq = sq <= 1 ? 1 : (sq <= 2 ? 2 : 4);
+        std::snprintf(buf, sizeof(buf), "fa_decode_rows_d%d_q%d", D, rq);
+    } else if (lp) {
         // 16-bit K/V streamed and widened in registers: 8-byte loads need d % 4 == 0
         const bool vec8 = (d % 4 == 0) && aligned8(q) && aligned8(k) && aligned8(v) && aligned16(out);
         std::snprintf(buf, sizeof(buf), "fa_decode_%s_d%d_%d", dtype == FA_DTYPE_BF16 ? "bf16" : "f16", D,

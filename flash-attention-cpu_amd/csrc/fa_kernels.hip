@@ -52,6 +52,10 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // reference that may trail the true row max by up to this much.
 constexpr float kLazyMax = 8.0f;
 
+#ifndef FA_DECODE_INTERLEAVE
+#define FA_DECODE_INTERLEAVE 1
+#endif
+
 // ---------------------------------------------------------------------------
 // Small device helpers
 // ---------------------------------------------------------------------------
@@ -924,10 +928,19 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
     const int qrow = q0 + lr;          // this lane's query (score column)
     const int qlast = min(seq_q, q0 + 16) - 1;
 
-    // This wave's keys.
+    // This wave's keys.  FA_DECODE_INTERLEAVE: wave w takes 16-key blocks
+    // w, w + 4, ... of the split (the workgroup streams one contiguous region
+    // of K and one of V); otherwise a contiguous quarter each.
+#if FA_DECODE_INTERLEAVE
+    const int kbeg = split * p.split_len + wave * 16;
+    const int kstep = 64;
+    int kend = min(seq_k, split * p.split_len + p.split_len);
+#else
     const int wave_len = p.split_len / 4;
     const int kbeg = split * p.split_len + wave * wave_len;
+    const int kstep = 16;
     int kend = min(seq_k, kbeg + wave_len);
+#endif
     if (causal) kend = min(kend, qlast + 1);
 
     // Q as the B operand: lane holds Q[qrow][16cc + 4lg + i] at qreg[4cc + i].
@@ -1031,19 +1044,19 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
             load_v(kb, va);
         }
         while (kb < kend) {
-            if (kb + 16 < kend) {
-                load_k(kb + 16, kb2);
-                load_v(kb + 16, vb2);
+            if (kb + kstep < kend) {
+                load_k(kb + kstep, kb2);
+                load_v(kb + kstep, vb2);
             }
             finish(kb, scores(kb, ka), va);
-            kb += 16;
+            kb += kstep;
             if (kb >= kend) break;
-            if (kb + 16 < kend) {
-                load_k(kb + 16, ka);
-                load_v(kb + 16, va);
+            if (kb + kstep < kend) {
+                load_k(kb + kstep, ka);
+                load_v(kb + kstep, va);
             }
             finish(kb, scores(kb, kb2), vb2);
-            kb += 16;
+            kb += kstep;
         }
     } else {
         R kk[NKL], vv[4 * NVL];
@@ -1051,12 +1064,12 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
             load_k(kbeg, kk);
             load_v(kbeg, vv);
         }
-        for (int kb = kbeg; kb < kend; kb += 16) {
-            const bool more = kb + 16 < kend;
+        for (int kb = kbeg; kb < kend; kb += kstep) {
+            const bool more = kb + kstep < kend;
             const f32x4 s = scores(kb, kk);
-            if (more) load_k(kb + 16, kk);   // K registers are free again
+            if (more) load_k(kb + kstep, kk);   // K registers are free again
             finish(kb, s, vv);
-            if (more) load_v(kb + 16, vv);   // V registers are free again
+            if (more) load_v(kb + kstep, vv);   // V registers are free again
         }
     }
 
@@ -1180,6 +1193,8 @@ __device__ __forceinline__ void merge_body(const FaParams& p) {
     for (int e = 0; e < 4; ++e)
         if (4 * ch + e < p.d) orow[4 * ch + e] = acc[e] * inv;
 }
+
+#include "fa_decode_rows.inc"
 
 // ---------------------------------------------------------------------------
 // Naive attention: the textbook three passes over a materialised score
@@ -1408,6 +1423,18 @@ FA_DECODE(256, 0, 1, 1)
     FA_DECODE_LP(256, TN, T, 0, 1, 1)
 FA_DECODE_LP_ALL(bf16, __bf16)
 FA_DECODE_LP_ALL(f16, _Float16)
+
+// fa_decode_rows_d{D}_q{RQ}: row-streaming split-KV decode for seq_q <= RQ
+// (f32, d % 4 == 0, 16-byte aligned operands).
+#define FA_DECODE_ROWS(D, RQ)                                                                    \
+    extern "C" __global__ void __launch_bounds__(256, 2) fa_decode_rows_d##D##_q##RQ(FaParams p) { \
+        decode_rows_body<D, RQ>(p);                                                              \
+    }
+#define FA_DECODE_ROWS_ALL(D) FA_DECODE_ROWS(D, 1) FA_DECODE_ROWS(D, 2) FA_DECODE_ROWS(D, 4)
+FA_DECODE_ROWS_ALL(32)
+FA_DECODE_ROWS_ALL(64)
+FA_DECODE_ROWS_ALL(128)
+FA_DECODE_ROWS_ALL(256)
 
 #define FA_MERGE(D) \
     extern "C" __global__ void __launch_bounds__(64) fa_merge_d##D(FaParams p) { merge_body<D>(p); }

@@ -49,6 +49,7 @@ FA_ERR_COPY = 11
 PATH_AUTO = 0
 PATH_PREFILL = 1
 PATH_SPLITKV = 2
+PATH_SPLITKV_ROWS = 3
 
 NAIVE_F32 = 0
 NAIVE_F64 = 1

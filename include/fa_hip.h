@@ -135,11 +135,16 @@ int fa_device_v3(void* stream, const float* q, const float* k, const float* v, s
  * 1/sqrt(d_head).  path: FA_PATH_AUTO (what fa_device_vN does),
  * FA_PATH_PREFILL (query-block kernel; with num_splits > 1 and v2/v3, each
  * block's keys are divided over num_splits workgroups whose partials are
- * merged), FA_PATH_SPLITKV (16-row decode tiles, always split; v2/v3 only).
+ * merged), FA_PATH_SPLITKV (16-row decode tiles, always split; v2/v3 only),
+ * FA_PATH_SPLITKV_ROWS (row-streaming split-KV for seq_len_q <= 4: K and V
+ * read as whole rows, dot products on the vector ALUs; v2/v3, f32, d_head %
+ * 4 == 0 and 16-byte aligned operands, else FA_ERR_UNSUPPORTED).  AUTO picks
+ * the row-streaming kernel for decode shapes it supports.
  * num_splits = 0 lets the library choose (at most 1024). */
 #define FA_PATH_AUTO 0
 #define FA_PATH_PREFILL 1
 #define FA_PATH_SPLITKV 2
+#define FA_PATH_SPLITKV_ROWS 3
 /* Element type of Q, K, V (O is always f32). */
 #define FA_DTYPE_F32 0
 #define FA_DTYPE_BF16 1

@@ -198,9 +198,24 @@ def test_planning_prefill_kernels():
 
 
 def test_planning_split_kv():
+    # seq_q <= 4: the row-streaming decode (whole-row K/V loads)
     s = describe(2, 1, 32, 1, 32768, 128, False)
-    assert s.startswith("fa_decode_d128_1 grid=16x1x32") and "fa_merge_d128 grid=32x1x1 block=64" in s
+    assert s.startswith("fa_decode_rows_d128_q1 grid=16x1x32 block=256") and "fa_merge_d128 grid=32x1x1 block=64" in s
     assert "splits=16 split_len=2048" in s
+    assert describe(3, 1, 32, 2, 32768, 64, False).startswith("fa_decode_rows_d64_q2 grid=16x1x32")
+    assert describe(2, 1, 8, 4, 9000, 256, True).startswith("fa_decode_rows_d256_q4")
+    assert describe(2, 1, 8, 5, 9000, 256, False).startswith("fa_decode_d256_1")   # 5 rows: 16-row tiles
+    assert describe(2, 1, 8, 1, 9000, 18, False).startswith("fa_decode_d32_0")     # d % 4 != 0: tiles
+    s = describe(2, 1, 32, 1, 32768, 128, False, fa.PATH_SPLITKV)                  # forced 16-row tiles
+    assert s.startswith("fa_decode_d128_1 grid=16x1x32") and "splits=16 split_len=2048" in s
+    assert describe(2, 1, 4, 3, 100, 64, False, fa.PATH_SPLITKV_ROWS, 2).startswith("fa_decode_rows_d64_q4 grid=2x1x4")
+    for bad in ((2, 1, 4, 5, 1000, 64), (2, 1, 4, 1, 1000, 18)):   # seq_q > 4; d % 4 != 0
+        with pytest.raises(fa.FaError) as e:
+            describe(*bad, False, fa.PATH_SPLITKV_ROWS)
+        assert e.value.status == fa.FA_ERR_UNSUPPORTED
+    with pytest.raises(fa.FaError) as e:
+        describe(1, 1, 4, 1, 1000, 64, False, fa.PATH_SPLITKV_ROWS)   # v1 never splits
+    assert e.value.status == fa.FA_ERR_INVALID_ARG
     assert "fa_decode" in describe(3, 1, 32, 16, 32768, 128, False)
     assert "fa_decode" not in describe(1, 1, 32, 16, 32768, 128, False)   # v1 keeps FA-1's loop
     assert "fa_decode" not in describe(2, 1, 32, 16, 256, 128, False)     # short keys: prefill

@@ -318,6 +318,52 @@ def test_split_kv_matches_oracle_and_prefill():
                 assert_parity(got, want, f"split-kv v{variant} splits={splits} {bh},{sq},{sk},{d},{causal}")
 
 
+def test_row_streaming_decode_matches_oracle():
+    """Row-streaming split-KV (seq_q <= 4, K/V read as whole rows, dot
+    products reduce-scattered across lanes): every padded head size, d below
+    the padded size (lanes past d), key ranges that end inside a key block and
+    splits whose waves get no keys, causal (only keys <= query row visible),
+    peaky logits, and a reference that moves mid-sequence."""
+    rng = np.random.default_rng(79)
+    cases = [(1, 1, 700, 128, False, 1.0), (3, 2, 1000, 128, False, 1.0), (2, 3, 333, 64, True, 1.0),
+             (1, 4, 513, 32, False, 1.0), (2, 1, 2048, 256, False, 1.0), (1, 3, 129, 40, False, 1.0),
+             (4, 1, 4096, 100, False, 3.0), (2, 4, 96, 128, True, 1.0), (2, 2, 1000, 256, False, 3.0),
+             (1, 1, 5, 64, False, 1.0), (3, 4, 777, 20, True, 1.0)]
+    for bh, sq, sk, d, causal, sigma in cases:
+        q = rng.standard_normal(bh * sq * d, dtype=np.float32) * np.float32(sigma)
+        k = rng.standard_normal(bh * sk * d, dtype=np.float32) * np.float32(sigma)
+        v = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+        for splits in (0, 1, 2, 3, 7, 40):
+            for variant in (2, 3):
+                tag = f"rows v{variant} splits={splits} {bh},{sq},{sk},{d},{causal},sigma={sigma}"
+                print("[case]", tag, flush=True)
+                got = _device_run(variant, q, k, v, bh, sq, sk, d, causal, fa.PATH_SPLITKV_ROWS, splits, guard=64)
+                assert_parity(got, want, tag)
+        desc = fa.describe_launch(2, 1, bh, sq, sk, d, causal, fa.PATH_SPLITKV_ROWS)
+        assert desc.startswith("fa_decode_rows_"), desc
+    # the key scale steps up after 64 keys: the lazy reference moves mid-sequence
+    bh, sk, d = 4, 3000, 128
+    for sq in (1, 4):
+        q = rng.standard_normal((bh, sq, d), dtype=np.float32)
+        ramp = np.where(np.arange(sk) < 64, 0.05, 2.4).astype(np.float32)[None, :, None]
+        k = (rng.standard_normal((bh, sk, d), dtype=np.float32) * ramp).astype(np.float32).ravel()
+        v = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        q = q.ravel()
+        want = cpu_v2(q, k, v, bh, sq, sk, d, False)
+        for splits in (0, 1, 5):
+            got = _device_run(2, q, k, v, bh, sq, sk, d, False, fa.PATH_SPLITKV_ROWS, splits, guard=64)
+            assert_parity(got, want, f"rows rising sq={sq} splits={splits}")
+    # AUTO picks it for decode shapes; shapes it cannot take are refused
+    assert fa.describe_launch(2, 1, 32, 1, 32768, 128, False).startswith("fa_decode_rows_d128_q1")
+    assert fa.describe_launch(3, 1, 32, 3, 32768, 64, False).startswith("fa_decode_rows_d64_q4")
+    assert fa.describe_launch(2, 1, 32, 16, 32768, 128, False).startswith("fa_decode_d128")
+    with pytest.raises(fa.FaError):
+        fa.describe_launch(2, 1, 4, 5, 1000, 128, False, fa.PATH_SPLITKV_ROWS)   # seq_q > 4
+    with pytest.raises(fa.FaError):
+        fa.describe_launch(2, 1, 4, 1, 1000, 17, False, fa.PATH_SPLITKV_ROWS)    # d % 4 != 0
+
+
 def test_key_split_prefill_matches_oracle():
     """v2/v3 query-block kernel with each block's keys divided over several
     workgroups and the partials merged (forced here; chosen automatically on
