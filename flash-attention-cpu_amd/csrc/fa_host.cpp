@@ -181,18 +181,19 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     const size_t rows = (size_t)(lp ? fa_lp_rows() : fa_prefill_rows(D));   // query rows per prefill workgroup
     const size_t nqb = (sq + rows - 1) / rows;
     const size_t nqt = (sq + kDecodeRows - 1) / kDecodeRows;
-    // Row-streaming decode: seq_q <= 4, f32, 128-bit loads.
-    const bool rows_ok = !lp && vec && sq <= (size_t)kRowsMaxQ;
+    // Row-streaming decode: 16-byte loads; f32 with seq_q <= 4, or 16-bit
+    // with seq_q = 1 and D >= 64.
+    const bool rows_ok = vec && (lp ? (sq == 1 && D >= 64) : sq <= (size_t)kRowsMaxQ);
     if (path == FA_PATH_SPLITKV_ROWS && !rows_ok) return FA_ERR_UNSUPPORTED;
     bool split = false;
     if (variant != 1) {
         if (path == FA_PATH_SPLITKV || path == FA_PATH_SPLITKV_ROWS) {
             split = true;
-        } else if (path == FA_PATH_AUTO && !lp) {
+        } else if (path == FA_PATH_AUTO) {
             // (16-bit inputs: the key-split 16-bit prefill is faster than the
-            // widening split-KV kernel -- 113 vs 148 us on config 4 -- so AUTO
-            // keeps the prefill; FA_PATH_SPLITKV still selects the decode.)
-            split = sq <= 64 && sk >= 512 && nqb * bh < (size_t)num_cus;
+            // 16-row widening split-KV kernel -- 113 vs 148 us on config 4 --
+            // so AUTO takes split-KV only where the row kernel applies.)
+            split = sq <= 64 && sk >= 512 && nqb * bh < (size_t)num_cus && (!lp || rows_ok);
         }
     }
     const bool row_decode = split && rows_ok && (path == FA_PATH_SPLITKV_ROWS || path == FA_PATH_AUTO);
@@ -337,7 +338,10 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     p.merge_scale = p.scale_log2e;   // decode partial maxima are raw scores
     if (row_decode) {
         const int rq = sq <= 1 ? 1 : (sq <= 2 ? 2 : 4);
-        std::snprintf(buf, sizeof(buf), "fa_decode_rows_d%d_q%d", D, rq);
+        if (lp)
+            std::snprintf(buf, sizeof(buf), "fa_decode_rows_%s_d%d_q1", dtype == FA_DTYPE_BF16 ? "bf16" : "f16", D);
+        else
+            std::snprintf(buf, sizeof(buf), "fa_decode_rows_d%d_q%d", D, rq);
     } else if (lp) {
         // 16-bit K/V streamed and widened in registers: 8-byte loads need d % 4 == 0
         const bool vec8 = (d % 4 == 0) && aligned8(q) && aligned8(k) && aligned8(v) && aligned16(out);

@@ -1435,6 +1435,15 @@ FA_DECODE_ROWS_ALL(32)
 FA_DECODE_ROWS_ALL(64)
 FA_DECODE_ROWS_ALL(128)
 FA_DECODE_ROWS_ALL(256)
+// fa_decode_rows_{bf16,f16}_d{D}_q1: 16-bit Q/K/V, seq_q = 1, d % 8 == 0,
+// D >= 64 (more query rows would spill the widened chunks).
+#define FA_DECODE_ROWS_LP(TN, T, D)                                                               \
+    extern "C" __global__ void __launch_bounds__(256, 2) fa_decode_rows_##TN##_d##D##_q1(FaParams p) { \
+        decode_rows_body<D, 1, T>(p);                                                            \
+    }
+#define FA_DECODE_ROWS_LP_ALL(TN, T) FA_DECODE_ROWS_LP(TN, T, 64) FA_DECODE_ROWS_LP(TN, T, 128) FA_DECODE_ROWS_LP(TN, T, 256)
+FA_DECODE_ROWS_LP_ALL(bf16, __bf16)
+FA_DECODE_ROWS_LP_ALL(f16, _Float16)
 
 #define FA_MERGE(D) \
     extern "C" __global__ void __launch_bounds__(64) fa_merge_d##D(FaParams p) { merge_body<D>(p); }

@@ -171,8 +171,11 @@ int fa_device_ex(int variant, void* stream, const float* q, const float* k, cons
  * 16-bit inputs (u = 2^-8 bf16, 2^-11 f16).  Causal masking, shape checks and
  * zero-dimension behaviour are those of fa_multihead_v2; d_head <= 256.  The
  * algorithm is v2/v3's (deferred normalisation, causal skip); no variant
- * argument.  opts: softmax_scale, path (AUTO or PREFILL) and num_splits as
- * for fa_device_ex; opts->dtype is ignored. */
+ * argument.  opts: softmax_scale, path and num_splits as for fa_device_ex;
+ * opts->dtype is ignored.  The split-KV kernels (FA_PATH_SPLITKV, and
+ * FA_PATH_SPLITKV_ROWS for seq_len_q = 1, d_head % 8 == 0, d_head > 32, which
+ * AUTO picks for decode steps) widen the 16-bit values exactly and compute in
+ * f32 without rounding the probabilities. */
 int fa_device_lp(int dtype, void* stream, const void* q, const void* k, const void* v, size_t batch,
                  size_t heads, size_t seq_len_q, size_t seq_len_k, size_t d_head,
                  const fa_config* config, const fa_launch_opts* opts, float* out);

@@ -213,6 +213,10 @@ def test_planning_split_kv():
         with pytest.raises(fa.FaError) as e:
             describe(*bad, False, fa.PATH_SPLITKV_ROWS)
         assert e.value.status == fa.FA_ERR_UNSUPPORTED
+    # 16-bit: seq_q = 1 and d % 8 == 0 with D >= 64 only
+    assert describe(2, 1, 32, 1, 32768, 128, False, dtype=fa.DTYPE_BF16).startswith("fa_decode_rows_bf16_d128_q1")
+    assert describe(2, 1, 32, 1, 32768, 256, False, dtype=fa.DTYPE_F16).startswith("fa_decode_rows_f16_d256_q1")
+    assert describe(2, 1, 32, 2, 32768, 128, False, dtype=fa.DTYPE_BF16).startswith("fa_prefill_lp_bf16")
     with pytest.raises(fa.FaError) as e:
         describe(1, 1, 4, 1, 1000, 64, False, fa.PATH_SPLITKV_ROWS)   # v1 never splits
     assert e.value.status == fa.FA_ERR_INVALID_ARG
@@ -291,8 +295,10 @@ def test_planning_16bit_inputs():
     assert describe(3, 1, 8, 16384, 16384, 128, True, dtype=fa.DTYPE_BF16).startswith("fa_prefill_lp_bf16_d128_2_t2")
     assert describe(2, 1, 2, 100, 100, 40, False, dtype=fa.DTYPE_F16).startswith("fa_prefill_lp_f16_d64_2_t1")
     assert describe(2, 1, 2, 100, 100, 20, False, dtype=fa.DTYPE_F16).startswith("fa_prefill_lp_f16_d32_0_t1")
-    s = describe(3, 1, 32, 1, 32768, 128, False, dtype=fa.DTYPE_BF16)   # AUTO: key-split 16-bit prefill
-    assert s.startswith("fa_prefill_lp_bf16_d128_2") and "fa_merge_d128 grid=32x1x1" in s
+    s = describe(3, 1, 32, 1, 32768, 128, False, dtype=fa.DTYPE_BF16)   # AUTO, seq_q 1: row-streaming decode
+    assert s.startswith("fa_decode_rows_bf16_d128_q1 grid=16x1x32") and "fa_merge_d128 grid=32x1x1" in s
+    s = describe(3, 1, 32, 4, 32768, 128, False, dtype=fa.DTYPE_BF16)   # AUTO, seq_q 4: key-split 16-bit prefill
+    assert s.startswith("fa_prefill_lp_bf16_d128_2") and "fa_merge_d128 grid=128x1x1" in s
     s = describe(3, 1, 32, 1, 32768, 128, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_BF16)   # split-KV, 16-bit loads
     assert s.startswith("fa_decode_bf16_d128_1 grid=16x1x32") and "fa_merge_d128 grid=32x1x1" in s
     assert describe(2, 1, 1, 4, 512, 64, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_F16).startswith("fa_decode_f16_d64_1")

@@ -223,3 +223,37 @@ def test_lp_split_kv_decode_is_exact_widening(dtype):
                 assert_lp(got, want, v32, dtype, what)
         got = lp_device(dtype, q16, k16, v16, bh, sq, sk, d, causal, fa.PATH_SPLITKV, 0, misalign=True)
         assert_parity(got, want, f"{NAME[dtype]} decode misaligned {bh}x{sq}x{sk} d={d}")
+
+
+@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16])
+def test_lp_row_streaming_decode_is_exact_widening(dtype):
+    """The row-streaming split-KV kernel (seq_q = 1, d % 8 == 0, d > 32)
+    widens 16-byte chunks of 8 16-bit values exactly and computes in f32: the
+    f32 bar against the oracle on the widened inputs.  Covers d below the
+    padded size (lanes past d), ragged key ranges, splits whose waves get no
+    keys, causal (only key 0 visible), and for f16 subnormal keys (scaled by
+    2^-20, mostly below 2^-14), which the widening must keep."""
+    from fa_testutil import assert_parity
+    rng = np.random.default_rng(41)
+    cases = [(32, 4096, 128, False, 1.0), (4, 777, 64, False, 1.0), (3, 1000, 256, False, 1.0),
+             (2, 513, 72, True, 1.0), (5, 2000, 200, False, 1.0), (2, 40, 128, False, 1.0),
+             (3, 1500, 128, False, 2.0 ** -20)]
+    for bh, sk, d, causal, kscale in cases:
+        sq = 1
+        q16, q32 = to16(rng.standard_normal(bh * sq * d, dtype=np.float32), dtype)
+        k16, k32 = to16(rng.standard_normal(bh * sk * d, dtype=np.float32) * np.float32(kscale), dtype)
+        v16, v32 = to16(rng.standard_normal(bh * sk * d, dtype=np.float32), dtype)
+        want = oracle.run(2, q32, k32, v32, bh, sq, sk, d, causal, 64, 128)
+        for path, splits in ((fa.PATH_SPLITKV_ROWS, 0), (fa.PATH_SPLITKV_ROWS, 1), (fa.PATH_SPLITKV_ROWS, 3),
+                             (fa.PATH_SPLITKV_ROWS, 40)):
+            plan = fa.describe_launch(2, 1, bh, sq, sk, d, causal, path, splits, dtype)
+            assert plan.startswith(f"fa_decode_rows_{NAME[dtype]}_"), plan
+            what = f"{NAME[dtype]} rows {bh}x{sq}x{sk} d={d} causal={causal} kscale={kscale} splits={splits}"
+            print("[case]", what, plan, flush=True)
+            assert_parity(lp_device(dtype, q16, k16, v16, bh, sq, sk, d, causal, path, splits), want, what)
+    # AUTO takes it for 16-bit decode steps; other shapes are refused on this path
+    assert fa.describe_launch(2, 1, 32, 1, 32768, 128, False, dtype=dtype).startswith(
+        f"fa_decode_rows_{NAME[dtype]}_d128_q1")
+    for bad in ((2, 1, 4, 2, 1000, 128), (2, 1, 4, 1, 1000, 32), (2, 1, 4, 1, 1000, 100)):   # sq 2; D 32; d % 8
+        with pytest.raises(fa.FaError):
+            fa.describe_launch(*bad, False, fa.PATH_SPLITKV_ROWS, 0, dtype)
