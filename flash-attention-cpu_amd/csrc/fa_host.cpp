@@ -24,7 +24,9 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <unordered_map>
+#include <vector>
 
 #include "../../include/fa_hip.h"
 #include "fa_params.h"
@@ -44,6 +46,18 @@ struct DeviceState {
     int num_cus = 256;
     std::mutex fn_mu;
     std::unordered_map<std::string, hipFunction_t> fns;
+    // Split workspaces (partials of split-KV / key split), one per stream,
+    // grow-only: kernels on one stream run in order, so consecutive calls on
+    // a stream can share one buffer, and calls on different streams never
+    // share.  Saves the stream-ordered allocate / free per call (measured:
+    // 5.5 us of idle GPU between back-to-back decode calls).
+    struct Workspace {
+        void* ptr = nullptr;
+        size_t bytes = 0;
+    };
+    std::mutex ws_mu;
+    std::unordered_map<std::string, Workspace> ws;
+    std::vector<void*> ws_retired;   // outgrown buffers: kept, a captured graph may name them
     // Host-slice calls: one staging allocation and stream per device.
     std::mutex io_mu;
     hipStream_t io_stream = nullptr;
@@ -375,6 +389,44 @@ int launch(int dev, const Launch& L, FaParams* p, hipStream_t stream) {
     return FA_OK;
 }
 
+// Largest split workspace kept per stream; larger ones are allocated and
+// released stream-ordered around the call.
+constexpr size_t kWorkspaceCacheMax = size_t(256) << 20;
+
+// The split workspace of `stream` on `dev`, at least `bytes` long.  Grows
+// geometrically with hipMalloc (not a stream operation, so a first call under
+// graph capture does not turn the buffer into graph-owned memory); an
+// outgrown buffer is kept, not freed, since work already queued on the stream
+// -- or a graph captured earlier -- may still use it.  hipStreamPerThread
+// names a different stream in every thread, so its key includes the thread.
+int stream_workspace(int dev, hipStream_t stream, size_t bytes, void** out) {
+    DeviceState& s = g_dev[dev];
+    char key[64];
+    if (stream == hipStreamPerThread) {
+        const size_t tid = std::hash<std::thread::id>{}(std::this_thread::get_id());
+        std::snprintf(key, sizeof(key), "pt:%zx", tid);
+    } else {
+        std::snprintf(key, sizeof(key), "%p", reinterpret_cast<void*>(stream));
+    }
+    std::lock_guard<std::mutex> lock(s.ws_mu);
+    DeviceState::Workspace& w = s.ws[key];
+    if (w.ptr && w.bytes >= bytes) {
+        *out = w.ptr;
+        return FA_OK;
+    }
+    const size_t want = std::max({bytes, 2 * w.bytes, size_t(1) << 20});
+    void* ptr = nullptr;
+    if (hipMalloc(&ptr, want) != hipSuccess) {
+        (void)hipGetLastError();
+        return FA_ERR_ALLOC;
+    }
+    if (w.ptr) s.ws_retired.push_back(w.ptr);
+    w.ptr = ptr;
+    w.bytes = want;
+    *out = ptr;
+    return FA_OK;
+}
+
 // Queue one attention call on device pointers.
 int run_device(int variant, hipStream_t stream, const void* q, const void* k, const void* v, size_t bh,
                size_t sq, size_t sk, size_t d, int causal, const fa_launch_opts* opts, float* out) {
@@ -390,8 +442,13 @@ int run_device(int variant, hipStream_t stream, const void* q, const void* k, co
     if (rc != FA_OK) return rc;
     if (!plan.split) return launch(dev, plan.first, &plan.p, stream);
 
+    const size_t bytes = plan.ws_floats * sizeof(float);
     float* ws = nullptr;
-    if (hipMallocAsync(reinterpret_cast<void**>(&ws), plan.ws_floats * sizeof(float), stream) != hipSuccess) {
+    const bool cached = bytes <= kWorkspaceCacheMax;
+    if (cached) {
+        rc = stream_workspace(dev, stream, bytes, reinterpret_cast<void**>(&ws));
+        if (rc != FA_OK) return rc;
+    } else if (hipMallocAsync(reinterpret_cast<void**>(&ws), bytes, stream) != hipSuccess) {
         (void)hipGetLastError();
         return FA_ERR_ALLOC;
     }
@@ -401,7 +458,7 @@ int run_device(int variant, hipStream_t stream, const void* q, const void* k, co
     plan.p.part_ml = ws + parts * 16 * D;
     rc = launch(dev, plan.first, &plan.p, stream);
     if (rc == FA_OK) rc = launch(dev, plan.second, &plan.p, stream);
-    if (hipFreeAsync(ws, stream) != hipSuccess) {
+    if (!cached && hipFreeAsync(ws, stream) != hipSuccess) {
         (void)hipGetLastError();
         if (rc == FA_OK) rc = FA_ERR_ALLOC;
     }

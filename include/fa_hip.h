@@ -116,8 +116,15 @@ int fa_attention_multihead(const float* q, size_t q_len, const float* k, size_t 
  * device-accessible memory), queued on `stream` (a hipStream_t; NULL = the
  * default stream).  No length checks are possible on raw pointers; zero
  * dims return FA_OK with nothing queued.  v2/v3 pick the split-KV
- * (flash-decoding) kernels for short query blocks against long key ranges;
- * its workspace is allocated stream-ordered and released after the merge.
+ * (flash-decoding) kernels for short query blocks against long key ranges,
+ * and a key split on grids smaller than the GPU.  Their partials go to a
+ * workspace kept per stream (up to 256 MiB; larger ones are allocated and
+ * released stream-ordered around the call): the first call on a stream that
+ * needs more allocates it with hipMalloc, and buffers are not freed before
+ * the process ends, so graphs captured with these calls stay valid.  Calls
+ * on one stream share its buffer in stream order; a stream handle value
+ * reused after hipStreamDestroy inherits the buffer, so synchronise a stream
+ * before destroying it if its handle may be reused for concurrent work.
  * These have no single counterpart in the reference (its API takes host
  * slices); they are the device form of the multihead entry points. */
 int fa_device_v1(void* stream, const float* q, const float* k, const float* v, size_t batch,

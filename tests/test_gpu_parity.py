@@ -521,3 +521,63 @@ def test_host_slice_calls_from_many_threads():
     assert not errors, errors
     for i, out in enumerate(results):
         assert np.array_equal(out, serial[i]), i
+
+
+def test_split_workspace_per_stream_and_graph_replay():
+    """Split partials live in a workspace kept per stream: calls queued on two
+    streams without synchronising in between must not share it, a later call
+    that needs a larger workspace must not disturb earlier queued ones, and a
+    captured graph of a decode call stays valid across replays (each replay
+    checked, with eager calls on other shapes between replays)."""
+    torch = _torch()
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(93)
+
+    def make(bh, sq, sk, d):
+        q = rng.standard_normal(bh * sq * d, dtype=np.float32)
+        k = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        v = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        t = [torch.from_numpy(a).to(dev) for a in (q, k, v)]
+        return (bh, sq, sk, d), (q, k, v), t, torch.zeros(bh * sq * d, device=dev)
+
+    small = [make(4, 1, 3000, 128), make(2, 16, 2000, 64), make(3, 3, 1500, 128)]
+    big = make(32, 1, 8192, 128)   # needs a larger workspace than any of the above
+    want = {}
+    for case in small + [big]:
+        (bh, sq, sk, d), (q, k, v), _, _ = case
+        want[id(case)] = cpu_v2(q, k, v, bh, sq, sk, d, False)
+
+    def queue(case, stream):
+        (bh, sq, sk, d), _, (tq, tk, tv), out = case
+        fa.attention_device(2, tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), 1, bh, sq, sk, d, False,
+                            out.data_ptr(), stream.cuda_stream)
+
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for i, case in enumerate(small):
+            queue(case, s1 if (i + rep) % 2 == 0 else s2)
+        queue(big, s1)              # grows s1's workspace while earlier calls may still run
+        queue(small[rep], s1)
+        torch.cuda.synchronize()
+        for case in small + [big]:
+            assert_parity(case[3].cpu().numpy(), want[id(case)], f"stream rep {rep} {case[0]}")
+
+    # graph capture of a decode call (workspace created before capture)
+    case = small[0]
+    gs = torch.cuda.Stream()
+    queue(case, gs)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=gs):
+        queue(case, gs)
+    for rep in range(4):
+        case[3].fill_(7.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_parity(case[3].cpu().numpy(), want[id(case)], f"graph replay {rep}")
+        queue(small[1 + rep % 2], gs)   # eager work on the capture stream between replays
+        queue(big, torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        assert_parity(small[1 + rep % 2][3].cpu().numpy(), want[id(small[1 + rep % 2])], f"eager after replay {rep}")
