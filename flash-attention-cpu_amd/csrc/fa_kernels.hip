@@ -55,6 +55,10 @@ constexpr float kLazyMax = 8.0f;
 #ifndef FA_DECODE_INTERLEAVE
 #define FA_DECODE_INTERLEAVE 1
 #endif
+// v3 prefill: only the upper half of the waves issue the stage DMA.
+#ifndef FA_FILL_HALF
+#define FA_FILL_HALF 1
+#endif
 
 // ---------------------------------------------------------------------------
 // Small device helpers
@@ -402,45 +406,56 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     // per-lane byte offsets that are the same for every stage, computed once
     // below -- no per-stage VALU address arithmetic.  The last, partial stage
     // takes the clamped per-lane path.
+    // Only the FW highest-numbered waves fill (all NW without the DMA
+    // loader).  Waves w and w + NW/2 share a SIMD and the lower-numbered one
+    // wins MFMA issue, so v3 leaves the stage's DMA to waves NW/2 .. NW-1:
+    // after each barrier their partners go straight to softmax and MFMA work
+    // while the fill instructions queue on the CU's load path.  Measured per
+    // wave (s_memtime): with every wave filling, each spent 0.9-1.3k cycles
+    // per stage issuing its DMA right after the barrier, with neither wave of
+    // a SIMD issuing MFMAs meanwhile.
+    constexpr int FW = (DMA && FA_FILL_HALF) ? NW / 2 : NW;
+    const int fwave = wave - (NW - FW);   // index among the filling waves; < 0: does not fill
     auto dma_geometry = [&](auto ld, int* voff) {
         constexpr int RCH = decltype(ld)::value / 4;   // chunks per padded row
         constexpr int TOTAL = SK * RCH;
         constexpr int RUNS = (TOTAL + 63) / 64;
-        constexpr int NI = (RUNS + NW - 1) / NW;
+        constexpr int NI = (RUNS + FW - 1) / FW;
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            const int pos = (i * NW + wave) * 64 + lane;
+            const int pos = (i * FW + fwave) * 64 + lane;
             const int r = pos / RCH, cidx = pos % RCH;
             const int col = (cidx < CPR && 4 * cidx < d) ? 4 * cidx : 0;
-            voff[i] = (pos < TOTAL) ? 4 * (r * d + col) : -1;   // -1: lane past the image
+            voff[i] = (fwave >= 0 && pos < TOTAL) ? 4 * (r * d + col) : -1;   // -1: lane past the image
         }
     };
     auto dma_stage = [&](auto ld, const float* __restrict__ src, int kbase, float* dst, const int* voff) {
         constexpr int RCH = decltype(ld)::value / 4;
         constexpr int TOTAL = SK * RCH;
         constexpr int RUNS = (TOTAL + 63) / 64;
-        constexpr int NI = (RUNS + NW - 1) / NW;
+        constexpr int NI = (RUNS + FW - 1) / FW;
+        if (fwave < 0) return;
         if (kbase + SK <= seq_k) {
             const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<float*>(src + (size_t)kbase * d), (short)0, SK * d * 4, 0x00020000);
             // LDS destinations from one opaque per-stage base: the compiler
             // would otherwise keep every run's address in its own SGPR.
-            int w256 = wave * 256;
+            int w256 = fwave * 256;
             asm volatile("" : "+s"(w256));
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
-                const int run = i * NW + wave;
-                // every wave has run i < RUNS while (i + 1) * NW <= RUNS;
+                const int run = i * FW + fwave;
+                // every filling wave has run i < RUNS while (i + 1) * FW <= RUNS;
                 // only the image's last run can have lanes past it
-                if (((i + 1) * NW <= RUNS || run < RUNS) && (TOTAL % 64 == 0 || run < RUNS - 1 || voff[i] >= 0))
+                if (((i + 1) * FW <= RUNS || run < RUNS) && (TOTAL % 64 == 0 || run < RUNS - 1 || voff[i] >= 0))
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                        rs, (__attribute__((address_space(3))) void*)(dst + i * NW * 256 + w256), 16, voff[i], 0, 0, 0);
+                        rs, (__attribute__((address_space(3))) void*)(dst + i * FW * 256 + w256), 16, voff[i], 0, 0, 0);
             }
         } else {
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
-                const int run = i * NW + wave;
-                if ((i + 1) * NW <= RUNS || run < RUNS) {
+                const int run = i * FW + fwave;
+                if ((i + 1) * FW <= RUNS || run < RUNS) {
                     const int pos = run * 64 + lane;
                     const int r = pos / RCH, cidx = pos % RCH;
                     const int key = min(kbase + r, seq_k - 1);
@@ -451,8 +466,8 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             }
         }
     };
-    constexpr int NI_K = ((SK * (LDK / 4) + 63) / 64 + NW - 1) / NW;
-    constexpr int NI_V = ((SK * (LDV / 4) + 63) / 64 + NW - 1) / NW;
+    constexpr int NI_K = ((SK * (LDK / 4) + 63) / 64 + FW - 1) / FW;
+    constexpr int NI_V = ((SK * (LDV / 4) + 63) / 64 + FW - 1) / FW;
     int voff_k[DMA ? NI_K : 1], voff_v[DMA ? NI_V : 1];
     if constexpr (DMA) {
         dma_geometry(std::integral_constant<int, LDK>{}, voff_k);
