@@ -203,11 +203,19 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     if (variant != 1) {
         if (path == FA_PATH_SPLITKV || path == FA_PATH_SPLITKV_ROWS) {
             split = true;
-        } else if (path == FA_PATH_AUTO) {
-            // (16-bit inputs: the key-split 16-bit prefill is faster than the
-            // 16-row widening split-KV kernel -- 113 vs 148 us on config 4 --
-            // so AUTO takes split-KV only where the row kernel applies.)
-            split = sq <= 64 && sk >= 512 && nqb * bh < (size_t)num_cus && (!lp || rows_ok);
+        } else if (path == FA_PATH_AUTO && nqb * bh < (size_t)num_cus) {
+            // Grids smaller than the GPU.  Decode shapes take split-KV.  So do
+            // small f32 prefills: at most num_cus/2 16-row tiles and 256 keys
+            // or more, where 16-row tiles x key splits occupy the GPU better
+            // than the key-split prefill (measured on MI355X: 2.0-3.8x faster
+            // up to 128 tiles x heads, e.g. config 1 20.6 -> 8.2 us; 0.5-0.8x
+            // from 188 on, where re-reading K / V per tile costs more).
+            // 16-bit inputs: the key-split 16-bit prefill is faster than the
+            // 16-row widening split-KV kernel (113 vs 148 us on config 4), so
+            // they take split-KV only where the row kernel applies.
+            const bool decode_shape = sq <= 64 && sk >= 512;
+            const bool few_tiles = !lp && nqt * bh * 2 <= (size_t)num_cus && sk >= 256;
+            split = (decode_shape || few_tiles) && (!lp || rows_ok);
         }
     }
     const bool row_decode = split && rows_ok && (path == FA_PATH_SPLITKV_ROWS || path == FA_PATH_AUTO);

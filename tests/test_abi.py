@@ -189,7 +189,7 @@ def test_planning_prefill_kernels():
     assert describe(1, 1, 32, 2048, 2048, 128, True).startswith("fa_prefill_v1_d128_1")
     assert describe(2, 1, 8, 16384, 16384, 128, True).startswith("fa_prefill_v2_d128_1 grid=1024x1x1")
     assert describe(2, 1, 16, 4096, 1024, 256, False).startswith("fa_prefill_v2_d256_1")
-    assert describe(2, 1, 1, 256, 256, 64, False).startswith("fa_prefill_v2_d64_1 grid=2x1x1")
+    assert describe(2, 1, 1, 256, 256, 64, False, fa.PATH_PREFILL).startswith("fa_prefill_v2_d64_1 grid=2x1x1")
     for d, pad in ((1, 32), (17, 32), (33, 64), (65, 128), (129, 256), (256, 256)):
         loader = 1 if d % 4 == 0 else 0
         assert describe(2, 1, 1, 100, 100, d, False).startswith(f"fa_prefill_v2_d{pad}_{loader}"), d
@@ -222,10 +222,17 @@ def test_planning_split_kv():
     assert e.value.status == fa.FA_ERR_INVALID_ARG
     assert "fa_decode" in describe(3, 1, 32, 16, 32768, 128, False)
     assert "fa_decode" not in describe(1, 1, 32, 16, 32768, 128, False)   # v1 keeps FA-1's loop
-    assert "fa_decode" not in describe(2, 1, 32, 16, 256, 128, False)     # short keys: prefill
+    assert "fa_decode" not in describe(2, 1, 32, 16, 200, 128, False)     # short keys: prefill
     assert "fa_decode" not in describe(2, 1, 32, 16, 32768, 128, False, fa.PATH_PREFILL)
     s = describe(2, 1, 1, 40, 300, 64, True, fa.PATH_SPLITKV, 3)
     assert s.startswith("fa_decode_d64_1 grid=3x3x1") and "splits=3 split_len=128" in s
+    # small f32 prefills (grid below the CU count, <= 128 tiles x heads, >= 256 keys): 16-row tiles
+    s = describe(2, 1, 1, 256, 256, 64, False)   # config 1
+    assert s.startswith("fa_decode_d64_1 grid=4x16x1") and "splits=4 split_len=64" in s
+    assert describe(3, 1, 1, 2048, 2048, 128, True).startswith("fa_decode_d128_1 grid=4x128x1")
+    assert describe(3, 1, 2, 2048, 2048, 128, True).startswith("fa_prefill_v3_d128_2")   # 256 tiles x heads
+    assert describe(3, 1, 1, 200, 200, 64, False).startswith("fa_prefill_v3_d64_2")      # fewer than 256 keys
+    assert describe(3, 1, 1, 256, 256, 64, False, dtype=fa.DTYPE_BF16).startswith("fa_prefill_lp_bf16")
 
 
 def test_planning_key_split_prefill():

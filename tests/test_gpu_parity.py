@@ -364,6 +364,26 @@ def test_row_streaming_decode_matches_oracle():
         fa.describe_launch(2, 1, 4, 1, 1000, 17, False, fa.PATH_SPLITKV_ROWS)    # d % 4 != 0
 
 
+def test_small_prefill_on_split_kv_tiles_matches_oracle():
+    """Grids smaller than the GPU with at most 128 16-row tiles x heads and
+    256+ keys run on the split-KV 16-row tiles (AUTO): long query ranges,
+    causal and ragged shapes, every padded head size; v2 and v3 agree."""
+    rng = np.random.default_rng(81)
+    cases = [(1, 2048, 2048, 128, True), (1, 1000, 1000, 128, False), (2, 300, 700, 64, True),
+             (4, 256, 1000, 256, True), (1, 777, 300, 40, False), (3, 500, 256, 32, True)]
+    for bh, sq, sk, d, causal in cases:
+        plan = fa.describe_launch(2, 1, bh, sq, sk, d, causal)
+        assert plan.startswith("fa_decode_d"), plan
+        q = rng.standard_normal(bh * sq * d, dtype=np.float32)
+        k = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        v = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+        for variant in (2, 3):
+            tag = f"small prefill v{variant} {bh},{sq},{sk},{d},{causal}"
+            print("[case]", tag, plan, flush=True)
+            assert_parity(_device_run(variant, q, k, v, bh, sq, sk, d, causal, guard=64), want, tag)
+
+
 def test_key_split_prefill_matches_oracle():
     """v2/v3 query-block kernel with each block's keys divided over several
     workgroups and the partials merged (forced here; chosen automatically on
