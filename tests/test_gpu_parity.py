@@ -197,6 +197,35 @@ def test_differential_fuzz_small_shapes():
             assert np.all(np.abs(out - want) < tol), f"it={it} v{variant} shape=({seq_q},{seq_k},{d}) mag={mag}"
 
 
+def test_differential_fuzz_split_paths():
+    """The fuzzer's magnitudes (10^0..10^6) and its tolerance on the shapes
+    that take the split paths: the row-streaming decode (seq_q <= 4), the
+    16-row split-KV tiles (decode shapes and small prefills) and the key-split
+    prefill, through AUTO and forced paths."""
+    rng = np.random.default_rng(4321)
+    for it in range(24):
+        sq = int(rng.choice([1, 2, 3, 4, 9, 16, 40, 300]))
+        sk = int(rng.integers(256, 3000))
+        d = int(rng.choice([8, 20, 32, 64, 100, 128, 256]))
+        bh = int(rng.integers(1, 4))
+        causal = bool(rng.integers(0, 2))
+        mag = float(10.0 ** rng.integers(0, 7))
+        q = (rng.uniform(-1, 1, bh * sq * d) * mag).astype(np.float32)
+        k = (rng.uniform(-1, 1, bh * sk * d) * mag).astype(np.float32)
+        v = (rng.uniform(-1, 1, bh * sk * d) * mag).astype(np.float32)
+        want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+        paths = [(fa.PATH_AUTO, 0), (fa.PATH_SPLITKV, 0), (fa.PATH_PREFILL, 3)]
+        if sq <= 4 and d % 4 == 0:
+            paths.append((fa.PATH_SPLITKV_ROWS, 0))
+        for path, splits in paths:
+            tag = f"it={it} path={path} ({bh},{sq},{sk},{d},{causal}) mag={mag}"
+            print("[case]", tag, flush=True)
+            out = _device_run(3, q, k, v, bh, sq, sk, d, causal, path, splits, guard=64)
+            assert np.array_equal(np.isfinite(out), np.isfinite(want)), tag
+            tol = 1e-1 * (np.maximum(np.abs(out), np.abs(want)) + 1.0)
+            assert np.all(np.abs(out - want) < tol), tag
+
+
 # ---------------------------------------------------------------------------
 # BASELINE.json configs
 # ---------------------------------------------------------------------------
