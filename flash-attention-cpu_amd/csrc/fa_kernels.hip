@@ -395,17 +395,13 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         }
     };
     // DMA: the stage image is SK rows of LD/4 chunks (the last ones are the
-    // pad); run R = i*NW + w (64 chunks = 1 KB) is written by wave w, lane L
-    // fetching the global chunk that belongs at image position 64R + L.
-    // Rows past seq_k are clamped to a real row (masked to -inf / multiplied
-    // by 0 later), columns past d and pad slots to column 0, so every read
-    // is in bounds.
-    //
-    // A full stage (every row below seq_k) is fetched with buffer loads: a
-    // per-stage buffer resource (base = the stage's first row, in SGPRs) and
-    // per-lane byte offsets that are the same for every stage, computed once
-    // below -- no per-stage VALU address arithmetic.  The last, partial stage
-    // takes the clamped per-lane path.
+    // pad); run R = i*FW + f (64 chunks = 1 KB) is written by filling wave f,
+    // lane L fetching the global chunk that belongs at image position 64R + L
+    // (columns past d and pad slots fetch column 0).  Every stage is fetched
+    // with buffer loads: a per-stage buffer resource (base = the stage's
+    // first row, range ending at seq_k, in SGPRs) and per-lane byte offsets
+    // that are the same for every stage, computed once below -- no per-stage
+    // VALU address arithmetic.
     // Only the FW highest-numbered waves fill (all NW without the DMA
     // loader).  Waves w and w + NW/2 share a SIMD and the lower-numbered one
     // wins MFMA issue, so v3 leaves the stage's DMA to waves NW/2 .. NW-1:
@@ -435,35 +431,25 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         constexpr int RUNS = (TOTAL + 63) / 64;
         constexpr int NI = (RUNS + FW - 1) / FW;
         if (fwave < 0) return;
-        if (kbase + SK <= seq_k) {
-            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<float*>(src + (size_t)kbase * d), (short)0, SK * d * 4, 0x00020000);
-            // LDS destinations from one opaque per-stage base: the compiler
-            // would otherwise keep every run's address in its own SGPR.
-            int w256 = fwave * 256;
-            asm volatile("" : "+s"(w256));
+        // The resource's range ends at seq_k: in the last, partial stage the
+        // rows past it read as zeros (measured on MI355X: out-of-range lanes
+        // of an LDS-DMA buffer load write 0 to LDS), and their scores are
+        // masked to -inf, so full and partial stages share one path.
+        const int rows = min(SK, seq_k - kbase);
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(src + (size_t)kbase * d), (short)0, rows * d * 4, 0x00020000);
+        // LDS destinations from one opaque per-stage base: the compiler
+        // would otherwise keep every run's address in its own SGPR.
+        int w256 = fwave * 256;
+        asm volatile("" : "+s"(w256));
 #pragma unroll
-            for (int i = 0; i < NI; ++i) {
-                const int run = i * FW + fwave;
-                // every filling wave has run i < RUNS while (i + 1) * FW <= RUNS;
-                // only the image's last run can have lanes past it
-                if (((i + 1) * FW <= RUNS || run < RUNS) && (TOTAL % 64 == 0 || run < RUNS - 1 || voff[i] >= 0))
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                        rs, (__attribute__((address_space(3))) void*)(dst + i * FW * 256 + w256), 16, voff[i], 0, 0, 0);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < NI; ++i) {
-                const int run = i * FW + fwave;
-                if ((i + 1) * FW <= RUNS || run < RUNS) {
-                    const int pos = run * 64 + lane;
-                    const int r = pos / RCH, cidx = pos % RCH;
-                    const int key = min(kbase + r, seq_k - 1);
-                    const int col = (cidx < CPR && 4 * cidx < d) ? 4 * cidx : 0;
-                    if (pos < TOTAL)
-                        __builtin_amdgcn_global_load_lds(src + (size_t)key * d + col, dst + run * 256, 16, 0, 0);
-                }
-            }
+        for (int i = 0; i < NI; ++i) {
+            const int run = i * FW + fwave;
+            // every filling wave has run i < RUNS while (i + 1) * FW <= RUNS;
+            // only the image's last run can have lanes past it
+            if (((i + 1) * FW <= RUNS || run < RUNS) && (TOTAL % 64 == 0 || run < RUNS - 1 || voff[i] >= 0))
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rs, (__attribute__((address_space(3))) void*)(dst + i * FW * 256 + w256), 16, voff[i], 0, 0, 0);
         }
     };
     constexpr int NI_K = ((SK * (LDK / 4) + 63) / 64 + FW - 1) / FW;
