@@ -587,7 +587,10 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     // Online-softmax update + PV for one stage (src/v2.rs:289-372; v1's
     // normalise / un-normalise round trip, src/v1.rs:291-385).  After
     // pv_preload(Vs).
-    auto softmax_pv = [&](f32x4* s, const float* Vs) {
+    // softmax_part: turns s into probabilities and updates m, l (rescaling
+    // o); pv_part: O^T += V^T P^T from them.  pv_hook(step) runs after each
+    // PV step's MFMAs and V read-ahead.
+    auto softmax_part = [&](f32x4* s) {
         // s holds S - m (S itself while m = -inf: nref was 0).
         float mt = fmax_fast(s[0][0], s[0][1]);
 #pragma unroll
@@ -644,6 +647,8 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             }
             l += ps;
         }
+    };
+    auto pv_part = [&](const f32x4* s, const float* Vs, auto&& pv_hook) {
         // O^T += V^T P^T: 4 keys per MFMA step (key 16b + 4g + r in lane group
         // g), a scheduling barrier per step.
         auto pv_step = [&](int step, const f32x4* vv) {
@@ -665,6 +670,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             for (int step = 0; step < 4 * KB; ++step) {
                 pv_step(step, vv[step % VR]);
                 if (step + PRE < 4 * KB) read_v(Vs, step + PRE, vv[(step + PRE) % VR]);
+                pv_hook(step);
                 __builtin_amdgcn_sched_barrier(0);
             }
         } else {
@@ -673,6 +679,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             for (int step = 0; step < 4 * KB; ++step) {
                 read_v(Vs, step, vv);
                 pv_step(step, vv);
+                pv_hook(step);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -682,6 +689,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             for (int j = 0; j < NOB; ++j) o[j] *= inv;
         }
     };
+    auto no_hook = [](int) {};
 
     // Is this wave's share of stage `st` worth computing?  v2/v3 skip stages
     // entirely in the future of every row of the wave; v1 does not.
@@ -755,17 +763,31 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         __syncthreads();
         if (ntot > 0) fill_stage(VL, Vh, kb_of(0), Vb0);
         if (ntot > 1) fill_stage(KL, Kh, kb_of(1), Kb1);
+        // Waves w and w + NW/2 share a SIMD and the lower-numbered one wins
+        // MFMA issue.  With the half fill, those (non-filling) waves take
+        // each stage's softmax right after its QK^T, before the barrier that
+        // ends the previous step -- while their partners still issue MFMAs --
+        // and begin every step with PV MFMAs; their partners keep the
+        // softmax at the start of the step, under the priority waves' MFMAs.
+        // Same operations in the same order per wave; only the barrier moves.
+        // Measured: d = 256 558.6 -> 548.9 us (config 5 shape), d = 64
+        // 144.3 -> 143.2 us.  Not at D = 128, where the two loop copies
+        // together need more than 256 VGPRs (39 spilled; 274 -> 288 us).
+        constexpr bool EARLY_OK = D != 128;
+        const bool early = EARLY_OK && FW < NW && fwave < 0;
         f32x4 s_cur[KB];
         bool act_cur = ntot > 0 && gstage_active(0);
         if (act_cur) {
             qk_preload(Kb0);
             qk_stage(Kb0, s_cur);
             mask_stage(s_cur, kb_of(0));
+            if (early) softmax_part(s_cur);
         }
         wait_vmcnt<0>();
         __syncthreads();   // V(0), K(1) resident; Kb0 free for K(2)
-        auto step = [&](auto parity, int gs) {
+        auto step = [&](auto parity, int gs, auto early_c) {
             constexpr int P = decltype(parity)::value;
+            constexpr bool EARLY = decltype(early_c)::value;
             float* k_fill = P ? Kb1 : Kb0;        // K(gs+2) -> buffer of K(gs)
             float* v_fill = P ? Vb0 : Vb1;        // V(gs+1)
             const float* k_next = P ? Kb0 : Kb1;  // K(gs+1)
@@ -776,13 +798,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             const bool switch_now = pairs && gs == nA - 1 && nB > 0;
             if (switch_now) load_q(q0_b + 16 * wave + li);
             const bool act_nxt = has_next && gstage_active(gs + 1);
-            // This stage's softmax + PV, then the next stage's QK^T from the
-            // other buffer, with no barrier between them.  Both stages are
-            // resident: their first operands are read before the softmax.
-            if (act_cur) pv_preload(v_cur);
-            if (act_nxt) qk_preload(k_next);
-            if (act_cur) softmax_pv(s_cur, v_cur);
-            if (switch_now) {
+            auto do_switch = [&]() {
                 // block A's rows, full 128-bit stores (two_blocks needs d = D)
                 const float lt = row4_sum(l);
                 const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
@@ -811,10 +827,44 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
                 l = 0.0f;
                 nref = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
                 scale_q();
-            }
-            if (act_nxt) {
-                qk_stage(k_next, s_cur);
-                mask_stage(s_cur, kb_of(gs + 1));
+            };
+            if constexpr (EARLY) {
+                // This stage's PV (probabilities from the previous step; the
+                // next K's first chunks are read during its last steps), then
+                // the next stage's QK^T and softmax.
+                if (act_cur) {
+                    pv_preload(v_cur);
+                    pv_part(s_cur, v_cur, [&](int step) {
+                        if constexpr (PRE > 0) {
+                            const int cc = step - (4 * KB - PRE);
+                            if (act_nxt && cc >= 0 && cc < NC) k_chunk(k_next, cc, kpre[cc]);
+                        }
+                    });
+                } else if (act_nxt) {
+                    qk_preload(k_next);
+                }
+                if (switch_now) do_switch();
+                if (act_nxt) {
+                    qk_stage(k_next, s_cur);
+                    mask_stage(s_cur, kb_of(gs + 1));
+                    softmax_part(s_cur);
+                }
+            } else {
+                // This stage's softmax + PV, then the next stage's QK^T from
+                // the other buffer, with no barrier between them.  Both stages
+                // are resident: their first operands are read before the
+                // softmax.
+                if (act_cur) pv_preload(v_cur);
+                if (act_nxt) qk_preload(k_next);
+                if (act_cur) {
+                    softmax_part(s_cur);
+                    pv_part(s_cur, v_cur, no_hook);
+                }
+                if (switch_now) do_switch();
+                if (act_nxt) {
+                    qk_stage(k_next, s_cur);
+                    mask_stage(s_cur, kb_of(gs + 1));
+                }
             }
             if (has_next) {
                 wait_vmcnt<0>();
@@ -822,10 +872,16 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             }
             act_cur = act_nxt;
         };
-        for (int gs = 0; gs < ntot; gs += 2) {
-            step(std::integral_constant<int, 0>{}, gs);
-            if (gs + 1 < ntot) step(std::integral_constant<int, 1>{}, gs + 1);
-        }
+        // One copy of the stage loop per order (a per-step branch between the
+        // two orders leaves the register allocator spilling).
+        auto run_steps = [&](auto early_c) {
+            for (int gs = 0; gs < ntot; gs += 2) {
+                step(std::integral_constant<int, 0>{}, gs, early_c);
+                if (gs + 1 < ntot) step(std::integral_constant<int, 1>{}, gs + 1, early_c);
+            }
+        };
+        if (early) run_steps(std::true_type{});
+        else run_steps(std::false_type{});
     } else {
         // Single LDS stage; the next stage's global loads are issued into
         // registers before the current stage computes.
@@ -848,7 +904,8 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
                 pv_preload(Vb0);
                 qk_stage(Kb0, s);
                 mask_stage(s, k0 + st * SK);
-                softmax_pv(s, Vb0);
+                softmax_part(s);
+                pv_part(s, Vb0, no_hook);
             }
             __syncthreads();
         }
