@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <condition_variable>
 #include <cstdio>
 #include <cstdlib>
 #include <algorithm>
@@ -39,6 +40,16 @@ constexpr int kDecodeRows = 16;     // query rows per split-KV wave
 constexpr int kDecodeWaves = 4;     // waves per split-KV workgroup
 constexpr int kRowsMaxQ = 4;        // row-streaming decode: most query rows
 
+// Host-slice staging: pageable host memory moves through a ring of pinned
+// buffers.  Host threads copy pageable <-> pinned while the DMA engine moves
+// the previous buffer.  Measured on the MI355X box: pageable hipMemcpyAsync
+// 25 GB/s host-to-device and 16 GB/s device-to-host; staged through 16 MiB
+// pinned chunks with 4 host threads 54 GB/s both ways.
+constexpr size_t kStageChunk = size_t(16) << 20;
+constexpr int kStageBufs = 4;
+constexpr int kCopyThreads = 4;     // host threads per staging copy, the caller included
+constexpr size_t kCopySplitMin = size_t(1) << 20;   // smaller copies stay on the caller
+
 struct DeviceState {
     std::once_flag once;
     int status = FA_OK;
@@ -58,12 +69,94 @@ struct DeviceState {
     std::mutex ws_mu;
     std::unordered_map<std::string, Workspace> ws;
     std::vector<void*> ws_retired;   // outgrown buffers: kept, a captured graph may name them
-    // Host-slice calls: one staging allocation and stream per device.
+    // Host-slice calls: one device staging allocation, one pinned ring and
+    // one stream per device.
     std::mutex io_mu;
     hipStream_t io_stream = nullptr;
     float* io_buf = nullptr;
     size_t io_floats = 0;
+    char* io_pin = nullptr;              // kStageBufs x kStageChunk pinned bytes
+    bool io_pin_tried = false;           // pinned ring unavailable: pageable copies
+    hipEvent_t io_ev[kStageBufs] = {};   // last DMA on each ring buffer
 };
+
+// A small pool of host threads for large memcpy's.  One copy at a time
+// (copy_mu); the caller takes the first part itself.
+class CopyPool {
+public:
+    explicit CopyPool(int workers) {
+        for (int i = 0; i < workers; ++i) threads_.emplace_back([this, i] { work(i + 1); });
+    }
+    ~CopyPool() {
+        {
+            std::lock_guard<std::mutex> l(mu_);
+            stop_ = true;
+        }
+        wake_.notify_all();
+        for (auto& t : threads_) t.join();
+    }
+    void copy(void* dst, const void* src, size_t n) {
+        if (threads_.empty() || n < kCopySplitMin) {
+            std::memcpy(dst, src, n);
+            return;
+        }
+        std::lock_guard<std::mutex> job(copy_mu_);
+        const int parts = static_cast<int>(threads_.size()) + 1;
+        {
+            std::lock_guard<std::mutex> l(mu_);
+            dst_ = static_cast<char*>(dst);
+            src_ = static_cast<const char*>(src);
+            n_ = n;
+            parts_ = parts;
+            pending_ = parts - 1;
+            ++gen_;
+        }
+        wake_.notify_all();
+        part(0, static_cast<char*>(dst), static_cast<const char*>(src), n, parts);
+        std::unique_lock<std::mutex> l(mu_);
+        done_.wait(l, [&] { return pending_ == 0; });
+    }
+
+private:
+    static void part(int id, char* dst, const char* src, size_t n, int parts) {
+        const size_t per = (n / parts + 63) / 64 * 64;
+        const size_t b = per * id;
+        if (b >= n) return;
+        std::memcpy(dst + b, src + b, std::min(per, n - b));
+    }
+    void work(int id) {
+        unsigned long seen = 0;
+        std::unique_lock<std::mutex> l(mu_);
+        for (;;) {
+            wake_.wait(l, [&] { return stop_ || gen_ != seen; });
+            if (stop_) return;
+            seen = gen_;
+            char* d = dst_;
+            const char* s = src_;
+            const size_t n = n_;
+            const int parts = parts_;
+            l.unlock();
+            part(id, d, s, n, parts);
+            l.lock();
+            if (--pending_ == 0) done_.notify_one();
+        }
+    }
+    std::vector<std::thread> threads_;
+    std::mutex copy_mu_, mu_;
+    std::condition_variable wake_, done_;
+    unsigned long gen_ = 0;
+    int pending_ = 0;
+    bool stop_ = false;
+    char* dst_ = nullptr;
+    const char* src_ = nullptr;
+    size_t n_ = 0;
+    int parts_ = 1;
+};
+
+CopyPool& copy_pool() {
+    static CopyPool pool(kCopyThreads - 1);
+    return pool;
+}
 
 DeviceState g_dev[kMaxDevices];
 
@@ -482,6 +575,80 @@ int check_single(size_t q_len, size_t k_len, size_t v_len, size_t out_len, size_
     return FA_OK;
 }
 
+// The pinned ring of `s` (allocated on first use; false when pinned memory
+// is unavailable, and host slices then take pageable copies).
+bool stage_ring(DeviceState& s) {
+    if (s.io_pin) return true;
+    if (s.io_pin_tried) return false;
+    s.io_pin_tried = true;
+    void* pin = nullptr;
+    if (hipHostMalloc(&pin, kStageBufs * kStageChunk, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    for (int b = 0; b < kStageBufs; ++b) {
+        if (hipEventCreateWithFlags(&s.io_ev[b], hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            for (int c = 0; c < b; ++c) (void)hipEventDestroy(s.io_ev[c]);
+            (void)hipHostFree(pin);
+            return false;
+        }
+    }
+    s.io_pin = static_cast<char*>(pin);
+    return true;
+}
+
+struct HostSeg {
+    char* dev;
+    const char* host;
+    size_t bytes;
+};
+
+// Host -> device through the pinned ring: each chunk is copied into a ring
+// buffer by the copy pool, then queued as a DMA on `st`; a buffer is refilled
+// once its previous DMA has completed.
+int stage_up(DeviceState& s, hipStream_t st, const HostSeg* segs, int nseg) {
+    int slot = 0;
+    bool used[kStageBufs] = {};
+    for (int i = 0; i < nseg; ++i) {
+        for (size_t off = 0; off < segs[i].bytes; off += kStageChunk) {
+            const size_t len = std::min(kStageChunk, segs[i].bytes - off);
+            char* buf = s.io_pin + slot * kStageChunk;
+            if (used[slot] && hipEventSynchronize(s.io_ev[slot]) != hipSuccess) return FA_ERR_COPY;
+            copy_pool().copy(buf, segs[i].host + off, len);
+            if (hipMemcpyAsync(segs[i].dev + off, buf, len, hipMemcpyHostToDevice, st) != hipSuccess ||
+                hipEventRecord(s.io_ev[slot], st) != hipSuccess)
+                return FA_ERR_COPY;
+            used[slot] = true;
+            slot = (slot + 1) % kStageBufs;
+        }
+    }
+    return FA_OK;
+}
+
+// Device -> host through the pinned ring: up to kStageBufs chunks in flight;
+// each is copied out by the copy pool when its DMA has completed.
+int stage_down(DeviceState& s, hipStream_t st, char* host, const char* dev, size_t bytes) {
+    const size_t nch = (bytes + kStageChunk - 1) / kStageChunk;
+    auto queue = [&](size_t c) {
+        const size_t off = c * kStageChunk, len = std::min(kStageChunk, bytes - off);
+        const int b = static_cast<int>(c % kStageBufs);
+        return hipMemcpyAsync(s.io_pin + b * kStageChunk, dev + off, len, hipMemcpyDeviceToHost, st) ==
+                       hipSuccess &&
+               hipEventRecord(s.io_ev[b], st) == hipSuccess;
+    };
+    for (size_t c = 0; c < nch && c < (size_t)kStageBufs; ++c)
+        if (!queue(c)) return FA_ERR_COPY;
+    for (size_t c = 0; c < nch; ++c) {
+        const int b = static_cast<int>(c % kStageBufs);
+        const size_t off = c * kStageChunk, len = std::min(kStageChunk, bytes - off);
+        if (hipEventSynchronize(s.io_ev[b]) != hipSuccess) return FA_ERR_COPY;
+        copy_pool().copy(host + off, s.io_pin + b * kStageChunk, len);
+        if (c + kStageBufs < nch && !queue(c + kStageBufs)) return FA_ERR_COPY;
+    }
+    return FA_OK;
+}
+
 // Host slices: copy in (Q/K/V elements of `esize` bytes), run
 // `run(stream, dq, dk, dv, dout)` on the device copies, copy the f32 output
 // out, synchronise.  Serialised per device.
@@ -523,23 +690,34 @@ int with_host_slices(const void* q, const void* k, const void* v, size_t esize, 
     void* dv = base + bq + bk;
     float* dout = reinterpret_cast<float*>(base + bq + 2 * bk);
     hipStream_t st = s.io_stream;
-    if (hipMemcpyAsync(dq, q, nq * esize, hipMemcpyHostToDevice, st) != hipSuccess ||
-        (nk > 0 && hipMemcpyAsync(dk, k, nk * esize, hipMemcpyHostToDevice, st) != hipSuccess) ||
-        (nk > 0 && hipMemcpyAsync(dv, v, nk * esize, hipMemcpyHostToDevice, st) != hipSuccess)) {
+    // On an error, queued DMA may still use the ring: drain the stream first.
+    auto fail = [&](int code) {
         (void)hipGetLastError();
         (void)hipStreamSynchronize(st);
-        return FA_ERR_COPY;
+        (void)hipGetLastError();
+        return code;
+    };
+    const bool staged = stage_ring(s);
+    if (staged) {
+        const HostSeg segs[3] = {{static_cast<char*>(dq), static_cast<const char*>(q), nq * esize},
+                                 {static_cast<char*>(dk), static_cast<const char*>(k), nk * esize},
+                                 {static_cast<char*>(dv), static_cast<const char*>(v), nk * esize}};
+        if (stage_up(s, st, segs, 3) != FA_OK) return fail(FA_ERR_COPY);
+    } else if (hipMemcpyAsync(dq, q, nq * esize, hipMemcpyHostToDevice, st) != hipSuccess ||
+               (nk > 0 && hipMemcpyAsync(dk, k, nk * esize, hipMemcpyHostToDevice, st) != hipSuccess) ||
+               (nk > 0 && hipMemcpyAsync(dv, v, nk * esize, hipMemcpyHostToDevice, st) != hipSuccess)) {
+        return fail(FA_ERR_COPY);
     }
     rc = run(st, dq, dk, dv, dout);
-    if (rc != FA_OK) {
-        (void)hipStreamSynchronize(st);
-        return rc;
+    if (rc != FA_OK) return fail(rc);
+    if (staged) {
+        if (stage_down(s, st, reinterpret_cast<char*>(out), reinterpret_cast<const char*>(dout),
+                       nq * sizeof(float)) != FA_OK)
+            return fail(FA_ERR_COPY);
+    } else if (hipMemcpyAsync(out, dout, nq * sizeof(float), hipMemcpyDeviceToHost, st) != hipSuccess) {
+        return fail(FA_ERR_COPY);
     }
-    if (hipMemcpyAsync(out, dout, nq * sizeof(float), hipMemcpyDeviceToHost, st) != hipSuccess ||
-        hipStreamSynchronize(st) != hipSuccess) {
-        (void)hipGetLastError();
-        return FA_ERR_COPY;
-    }
+    if (hipStreamSynchronize(st) != hipSuccess) return fail(FA_ERR_COPY);
     return FA_OK;
 }
 
