@@ -84,8 +84,13 @@ struct DeviceState {
 // (copy_mu); the caller takes the first part itself.
 class CopyPool {
 public:
+    // Threads that cannot be started leave the pool smaller (with none, the
+    // caller copies alone); no exception leaves the C ABI.
     explicit CopyPool(int workers) {
-        for (int i = 0; i < workers; ++i) threads_.emplace_back([this, i] { work(i + 1); });
+        try {
+            for (int i = 0; i < workers; ++i) threads_.emplace_back([this, i] { work(i + 1); });
+        } catch (...) {
+        }
     }
     ~CopyPool() {
         {
