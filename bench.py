@@ -199,7 +199,8 @@ def main() -> int:
 
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X; "
-              "heads shard across GPUs with no communication (see DESIGN.md), run with --gpus 1",
+              "heads would shard across GPUs with no communication, each GPU running this kernel on "
+              "its share; run with --gpus 1",
               file=sys.stderr)
         return 2
 
