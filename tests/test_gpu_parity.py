@@ -579,7 +579,8 @@ def test_host_slices_staged_copies_match_device_api():
     chunks (O of 18 MB) and copies under and over the 1 MiB threading cut.
     The host-slice call runs the same kernels on the same data as the device
     call, so the outputs agree bit for bit."""
-    cases = [(3, 1111, 30001, 100, False), (5, 9001, 300, 100, True), (1, 7, 5, 3, False)]
+    cases = [(3, 1111, 30001, 100, False), (5, 9001, 300, 100, True), (1, 7, 5, 3, False),
+             (32, 2048, 2048, 128, True), (5, 16384, 512, 128, False)]
     for i, (bh, sq, sk, d, causal) in enumerate(cases):
         q, k, v = random_vec(bh * sq * d, 40 + i), random_vec(bh * sk * d, 50 + i), random_vec(bh * sk * d, 60 + i)
         host = np.full(bh * sq * d, 7.0, np.float32)
@@ -587,21 +588,22 @@ def test_host_slices_staged_copies_match_device_api():
         dev = _device_run(2, q, k, v, bh, sq, sk, d, causal)
         assert np.array_equal(host, dev), (bh, sq, sk, d, causal)
     # 16-bit inputs: an odd number of elements per tensor, a K/V upload over
-    # several chunks.
+    # several chunks; config 2 in bf16.
     torch = _torch()
-    bh, sq, sk, d = 1, 3, 4194305, 3
-    q16 = fa.f32_to_bf16_bits(random_vec(bh * sq * d, 70))
-    k16 = fa.f32_to_bf16_bits(random_vec(bh * sk * d, 71))
-    v16 = fa.f32_to_bf16_bits(random_vec(bh * sk * d, 72))
-    host = np.full(bh * sq * d, 7.0, np.float32)
-    fa.flash_attention_multihead_lp(fa.DTYPE_BF16, q16, k16, v16, 1, bh, sq, sk, d, None, host)
     dev = torch.device("cuda", 0)
-    t16 = [torch.from_numpy(a.view(np.int16)).to(dev) for a in (q16, k16, v16)]
-    out = torch.zeros(bh * sq * d, device=dev)
-    fa.attention_device_lp(fa.DTYPE_BF16, t16[0].data_ptr(), t16[1].data_ptr(), t16[2].data_ptr(), 1, bh, sq, sk, d,
-                           False, out.data_ptr(), torch.cuda.current_stream().cuda_stream)
-    torch.cuda.synchronize()
-    assert np.array_equal(host, out.cpu().numpy())
+    for i, (bh, sq, sk, d, causal) in enumerate([(1, 3, 4194305, 3, False), (32, 2048, 2048, 128, True)]):
+        q16 = fa.f32_to_bf16_bits(random_vec(bh * sq * d, 70 + i))
+        k16 = fa.f32_to_bf16_bits(random_vec(bh * sk * d, 72 + i))
+        v16 = fa.f32_to_bf16_bits(random_vec(bh * sk * d, 74 + i))
+        host = np.full(bh * sq * d, 7.0, np.float32)
+        fa.flash_attention_multihead_lp(fa.DTYPE_BF16, q16, k16, v16, 1, bh, sq, sk, d,
+                                        fa.FlashAttentionConfig(causal=causal), host)
+        t16 = [torch.from_numpy(a.view(np.int16)).to(dev) for a in (q16, k16, v16)]
+        out = torch.zeros(bh * sq * d, device=dev)
+        fa.attention_device_lp(fa.DTYPE_BF16, t16[0].data_ptr(), t16[1].data_ptr(), t16[2].data_ptr(), 1, bh, sq, sk,
+                               d, causal, out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert np.array_equal(host, out.cpu().numpy()), (bh, sq, sk, d, causal)
 
 
 def test_split_workspace_per_stream_and_graph_replay():
