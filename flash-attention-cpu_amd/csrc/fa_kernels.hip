@@ -489,8 +489,10 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     // work (the stage is already resident), so their LDS latency is hidden;
     // inside QK^T and PV the reads then run PRE chunks / steps ahead through
     // a ring of PRE + 1 register sets, each read issued after the MFMAs that
-    // last used its slot.  D = 256 has no registers to spare: one ahead.
-    constexpr int PRE = (D <= 128) ? 2 : 0;
+    // last used its slot.  D = 256: v2 runs one ahead (230 VGPRs; config 5's
+    // shape 577 -> 572.5 us); v1 gains nothing and v3, with its second K / V
+    // buffer, would spill, so they read each operand just before its MFMA.
+    constexpr int PRE = (D <= 128) ? 2 : (VARIANT == 2 ? 1 : 0);
     f32x4 kpre[PRE ? PRE : 1][KB];
     auto k_chunk = [&](const float* Ks, int cc, f32x4* dst) {
 #pragma unroll
