@@ -533,11 +533,32 @@ int stream_workspace(int dev, hipStream_t stream, size_t bytes, void** out) {
     return FA_OK;
 }
 
+int run_naive_device(hipStream_t stream, const float* q, const float* k, const float* v, size_t bh, size_t sq,
+                     size_t sk, size_t d, int causal, int precision, float* out, float scale);
+
+// Heads wider than the flash kernels' 256 columns (the crate takes any
+// d_head): f32 inputs on the automatic path run the naive kernels over a
+// materialised score matrix (src/naive.rs:14-75, in f32 with the same
+// 1/sqrt(d) or explicit scale).  FA_OK when that applies, else the status.
+int wide_head_status(int variant, const fa_launch_opts* opts) {
+    if (variant < 1 || variant > 3) return FA_ERR_INVALID_ARG;
+    if (opts && (opts->dtype != FA_DTYPE_F32 || opts->path != FA_PATH_AUTO || opts->num_splits > 0))
+        return FA_ERR_UNSUPPORTED;
+    return FA_OK;
+}
+
 // Queue one attention call on device pointers.
 int run_device(int variant, hipStream_t stream, const void* q, const void* k, const void* v, size_t bh,
                size_t sq, size_t sk, size_t d, int causal, const fa_launch_opts* opts, float* out) {
     if (bh == 0 || sq == 0 || sk == 0 || d == 0) return FA_OK;   // src/common.rs:56
     if (!q || !k || !v || !out) return FA_ERR_INVALID_ARG;
+    if (d > (size_t)kMaxD) {
+        const int rc = wide_head_status(variant, opts);
+        if (rc != FA_OK) return rc;
+        return run_naive_device(stream, static_cast<const float*>(q), static_cast<const float*>(k),
+                                static_cast<const float*>(v), bh, sq, sk, d, causal, FA_NAIVE_F32, out,
+                                opts ? opts->softmax_scale : 0.0f);
+    }
     int dev;
     int rc = current_device(&dev);
     if (rc != FA_OK) return rc;
@@ -758,7 +779,7 @@ int launch_naive(int dev, const char* name, unsigned gx, unsigned gy, unsigned g
 }
 
 int run_naive_device(hipStream_t stream, const float* q, const float* k, const float* v, size_t bh, size_t sq,
-                     size_t sk, size_t d, int causal, int precision, float* out) {
+                     size_t sk, size_t d, int causal, int precision, float* out, float scale) {
     // The crate writes out = 0 when seq_len_k == 0 (every row's fill(0.0),
     // src/naive.rs:64); nothing is written when seq_len_q or d_head is 0.
     if (bh == 0 || sq == 0 || d == 0) return FA_OK;
@@ -802,6 +823,10 @@ int run_naive_device(hipStream_t stream, const float* q, const float* k, const f
         p.causal = causal ? 1 : 0;
         p.scale_f = 1.0f / std::sqrt(static_cast<float>(d));   // src/naive.rs:29
         p.scale_d = 1.0 / std::sqrt(static_cast<double>(d));
+        if (scale > 0.0f && std::isfinite(scale)) {
+            p.scale_f = scale;
+            p.scale_d = static_cast<double>(scale);
+        }
         const unsigned gq = static_cast<unsigned>((sq + 63) / 64);
         if (sk > 0) {
             rc = launch_naive(dev, n_scores.c_str(), static_cast<unsigned>((sk + 63) / 64), gq,
@@ -854,7 +879,7 @@ const char* fa_status_string(int status) {
         case FA_ERR_V_SHAPE: return "v shape mismatch";
         case FA_ERR_OUT_SHAPE: return "out shape mismatch";
         case FA_ERR_INVALID_ARG: return "invalid argument";
-        case FA_ERR_UNSUPPORTED: return "unsupported shape (d_head > 256 or size beyond 32-bit indexing)";
+        case FA_ERR_UNSUPPORTED: return "unsupported shape (d_head > 256 off the automatic f32 path, or size beyond 32-bit indexing)";
         case FA_ERR_NO_DEVICE: return "no HIP device available";
         case FA_ERR_MODULE: return "cannot load the gfx950 code object (fa_kernels.hsaco / FA_HIP_MODULE)";
         case FA_ERR_ALLOC: return "device allocation failed";
@@ -944,14 +969,14 @@ int fa_naive_attention(const float* q, size_t q_len, const float* k, size_t k_le
                             [&](hipStream_t st, const void* dq, const void* dk, const void* dv, float* dout) {
                                 return run_naive_device(st, static_cast<const float*>(dq), static_cast<const float*>(dk),
                                                         static_cast<const float*>(dv), 1, sq, sk, d, causal,
-                                                        FA_NAIVE_F32, dout);
+                                                        FA_NAIVE_F32, dout, 0.0f);
                             });
 }
 
 int fa_naive_device(void* stream, const float* q, const float* k, const float* v, size_t batch, size_t heads,
                     size_t sq, size_t sk, size_t d, int causal, int precision, float* out) {
     return run_naive_device(static_cast<hipStream_t>(stream), q, k, v, batch * heads, sq, sk, d, causal, precision,
-                            out);
+                            out, 0.0f);
 }
 
 int fa_device_ex(int variant, void* stream, const float* q, const float* k, const float* v, size_t batch,
@@ -1011,8 +1036,14 @@ int fa_describe_launch(int variant, size_t batch, size_t heads, size_t sq, size_
         Plan plan;
         // Alignment is assumed (device allocations are 256-byte aligned).
         static const float dummy[4] __attribute__((aligned(16))) = {0, 0, 0, 0};
-        rc = make_plan(variant, dummy, dummy, dummy, dummy, bh, sq, sk, d, causal, opts, num_cus, &plan);
-        if (rc == FA_OK) {
+        if (d > (size_t)kMaxD) {
+            rc = wide_head_status(variant, opts);
+            if (rc == FA_OK)
+                text = "fa_naive_scores_f32; fa_naive_softmax_f32; fa_naive_pv_f32 (d_head > 256: materialised scores)";
+        } else {
+            rc = make_plan(variant, dummy, dummy, dummy, dummy, bh, sq, sk, d, causal, opts, num_cus, &plan);
+        }
+        if (rc == FA_OK && d <= (size_t)kMaxD) {
             char tmp[256];
             std::snprintf(tmp, sizeof(tmp), "%s grid=%ux%ux%u block=%u", plan.first.name.c_str(), plan.first.gx,
                           plan.first.gy, plan.first.gz, plan.first.bx);

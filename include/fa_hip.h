@@ -37,7 +37,9 @@ extern "C" {
 #define FA_ERR_V_SHAPE 3      /* "v shape mismatch"   src/common.rs:53, :89 */
 #define FA_ERR_OUT_SHAPE 4    /* "out shape mismatch" src/common.rs:54, :90 */
 #define FA_ERR_INVALID_ARG 5  /* NULL pointer with a non-zero length, bad variant/option */
-#define FA_ERR_UNSUPPORTED 6  /* d_head > 256, or a size beyond 32-bit row indexing */
+#define FA_ERR_UNSUPPORTED 6  /* d_head > 256 with 16-bit inputs or a forced path / split
+                                 count, or a size beyond 32-bit row indexing (f32 heads wider
+                                 than 256 on the automatic path run the naive kernels) */
 #define FA_ERR_NO_DEVICE 7    /* no HIP device visible */
 #define FA_ERR_MODULE 8       /* code object missing / unloadable (FA_HIP_MODULE) */
 #define FA_ERR_ALLOC 9        /* device allocation failed */

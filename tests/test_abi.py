@@ -252,9 +252,13 @@ def test_planning_key_split_prefill():
 
 
 def test_planning_errors():
-    with pytest.raises(fa.FaError) as e:
-        describe(2, 1, 1, 10, 10, 257, False)
-    assert e.value.status == fa.FA_ERR_UNSUPPORTED
+    # f32 heads wider than the flash kernels' 256 columns: the naive kernels
+    # on the automatic path; forced paths and 16-bit inputs are refused
+    assert describe(2, 1, 1, 10, 10, 257, False).startswith("fa_naive_scores_f32")
+    for kw in ({"path": fa.PATH_PREFILL}, {"path": fa.PATH_SPLITKV}, {"dtype": fa.DTYPE_BF16}):
+        with pytest.raises(fa.FaError) as e:
+            describe(2, 1, 1, 10, 10, 257, False, **kw)
+        assert e.value.status == fa.FA_ERR_UNSUPPORTED, kw
     with pytest.raises(fa.FaError) as e:
         describe(1, 1, 1, 10, 1000, 64, False, fa.PATH_SPLITKV)
     assert e.value.status == fa.FA_ERR_INVALID_ARG

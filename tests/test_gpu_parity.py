@@ -84,6 +84,27 @@ def test_every_padded_head_dim(variant):
 
 
 @pytest.mark.parametrize("variant", ALL_VARIANTS)
+def test_heads_wider_than_256(variant):
+    # The crate takes any d_head; past the flash kernels' 256 columns the
+    # automatic f32 path runs the naive kernels (materialised scores).
+    for d in (257, 300, 512):
+        run_case(variant, 70, 90, d, 64, 128, d % 2 == 1)
+    bh, sq, sk, d = 3, 65, 129, 320
+    q, k, v = random_vec(bh * sq * d, 4), random_vec(bh * sk * d, 5), random_vec(bh * sk * d, 6)
+    want = cpu_v2(q, k, v, bh, sq, sk, d, True)
+    out = np.zeros(bh * sq * d, np.float32)
+    fa.MULTIHEAD_VARIANTS[variant](q, k, v, 1, bh, sq, sk, d, fa.FlashAttentionConfig(causal=True), out)
+    assert_parity(out, want, f"v{variant} multihead d={d}")
+    assert_parity(_device_run(variant, q, k, v, bh, sq, sk, d, True, guard=64), want, f"v{variant} device d={d}")
+    # explicit scale: attention with scale s equals default attention on Q * (s * sqrt(d))
+    scale = 0.03
+    q2 = (q.astype(np.float64) * scale * np.sqrt(d)).astype(np.float32)
+    want2 = np.concatenate([attention_f64(q2[h * sq * d:(h + 1) * sq * d], k[h * sk * d:(h + 1) * sk * d],
+                                          v[h * sk * d:(h + 1) * sk * d], sq, sk, d, True) for h in range(bh)])
+    assert max_abs_diff(_device_run(variant, q, k, v, bh, sq, sk, d, True, scale=scale), want2) < 1e-5
+
+
+@pytest.mark.parametrize("variant", ALL_VARIANTS)
 def test_multihead_matches_per_head(variant):
     batch, heads, seq_q, seq_k, d = 2, 3, 37, 50, 16
     q = random_vec(batch * heads * seq_q * d, 21)
