@@ -49,6 +49,10 @@ constexpr size_t kStageChunk = size_t(16) << 20;
 constexpr int kStageBufs = 4;
 constexpr int kCopyThreads = 4;     // host threads per staging copy, the caller included
 constexpr size_t kCopySplitMin = size_t(1) << 20;   // smaller copies stay on the caller
+// Transfers below this many bytes take plain pageable copies: the ring's
+// per-chunk events cost more than they save on small calls (measured: a
+// 256 x 64 single-head call 78 -> 111 us through the ring).
+constexpr size_t kStageMinBytes = size_t(2) << 20;
 
 struct DeviceState {
     std::once_flag once;
@@ -723,8 +727,9 @@ int with_host_slices(const void* q, const void* k, const void* v, size_t esize, 
         (void)hipGetLastError();
         return code;
     };
-    const bool staged = stage_ring(s);
-    if (staged) {
+    const bool staged_up = (nq + 2 * nk) * esize >= kStageMinBytes && stage_ring(s);
+    const bool staged_down = nq * sizeof(float) >= kStageMinBytes && stage_ring(s);
+    if (staged_up) {
         const HostSeg segs[3] = {{static_cast<char*>(dq), static_cast<const char*>(q), nq * esize},
                                  {static_cast<char*>(dk), static_cast<const char*>(k), nk * esize},
                                  {static_cast<char*>(dv), static_cast<const char*>(v), nk * esize}};
@@ -736,7 +741,7 @@ int with_host_slices(const void* q, const void* k, const void* v, size_t esize, 
     }
     rc = run(st, dq, dk, dv, dout);
     if (rc != FA_OK) return fail(rc);
-    if (staged) {
+    if (staged_down) {
         if (stage_down(s, st, reinterpret_cast<char*>(out), reinterpret_cast<const char*>(dout),
                        nq * sizeof(float)) != FA_OK)
             return fail(FA_ERR_COPY);
