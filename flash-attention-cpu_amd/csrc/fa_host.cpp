@@ -30,6 +30,7 @@
 #include <vector>
 
 #include "../../include/fa_hip.h"
+#include "fa_copy_parts.h"
 #include "fa_params.h"
 
 namespace {
@@ -128,10 +129,9 @@ public:
 
 private:
     static void part(int id, char* dst, const char* src, size_t n, int parts) {
-        const size_t per = (n / parts + 63) / 64 * 64;
-        const size_t b = per * id;
-        if (b >= n) return;
-        std::memcpy(dst + b, src + b, std::min(per, n - b));
+        size_t b, len;
+        fa_copy_part_range(n, parts, id, &b, &len);
+        if (len) std::memcpy(dst + b, src + b, len);
     }
     void work(int id) {
         unsigned long seen = 0;
@@ -1013,6 +1013,7 @@ int fa_multihead_lp(int dtype, const void* q, size_t q_len, const void* k, size_
     if (out_len != bh * sq * d) return FA_ERR_OUT_SHAPE;
     if (bh == 0 || sq == 0 || sk == 0 || d == 0) return FA_OK;   // out untouched
     if (!q || !k || !v || !out) return FA_ERR_INVALID_ARG;
+    if (d > (size_t)kMaxD) return FA_ERR_UNSUPPORTED;   // before any copy: the 16-bit kernels stop at 256
     const int causal = cfg ? cfg->causal : 0;
     const fa_launch_opts o{0.0f, FA_PATH_AUTO, 0, dtype};
     return with_host_slices(q, k, v, 2, bh, sq, sk, d, out,

@@ -320,3 +320,16 @@ def test_planning_16bit_inputs():
     with pytest.raises(fa.FaError) as e:
         describe(3, 1, 1, 4, 512, 64, False, dtype=7)
     assert e.value.status == fa.FA_ERR_INVALID_ARG
+
+
+def test_lp_host_slices_reject_wide_heads_before_copying():
+    """fa_multihead_lp with d_head > 256 is refused right after the shape
+    checks: no device access (so no FA_ERR_NO_DEVICE here), out untouched."""
+    bh, sq, sk, d = 1, 3, 5, 300
+    q = np.zeros(bh * sq * d, np.uint16)
+    k = np.zeros(bh * sk * d, np.uint16)
+    out = np.full(bh * sq * d, 3.0, np.float32)
+    with pytest.raises(fa.FaError) as e:
+        fa.flash_attention_multihead_lp(fa.DTYPE_BF16, q, k, k, 1, bh, sq, sk, d, None, out)
+    assert e.value.status == fa.FA_ERR_UNSUPPORTED
+    assert np.all(out == 3.0)

@@ -627,6 +627,35 @@ def test_host_slices_staged_copies_match_device_api():
         assert np.array_equal(host, out.cpu().numpy()), (bh, sq, sk, d, causal)
 
 
+def test_host_slices_odd_16bit_counts_copy_every_byte():
+    """K and V of 15969 x 33 bf16 values are 1053954 bytes each (256m + 2):
+    the copy pool splits them over four threads, and every byte must reach the
+    device.  A first call with other values leaves different bytes in the
+    pinned ring, so a piece the partition skipped would show as a stale last
+    element (the large last K / V values make that visible) and the host-slice
+    output would differ from the device API's."""
+    torch = _torch()
+    dev = torch.device("cuda", 0)
+    bh, sq, sk, d = 1, 64, 15969, 33
+    q16 = fa.f32_to_bf16_bits(random_vec(bh * sq * d, 81))
+    k = random_vec(bh * sk * d, 82)
+    v = random_vec(bh * sk * d, 83)
+    k[-1], v[-1] = 6.0, 40.0
+    k16, v16 = fa.f32_to_bf16_bits(k), fa.f32_to_bf16_bits(v)
+    junk = np.full(bh * sq * d, 7.0, np.float32)
+    fa.flash_attention_multihead_lp(fa.DTYPE_BF16, q16, fa.f32_to_bf16_bits(-k), fa.f32_to_bf16_bits(-v), 1, bh,
+                                    sq, sk, d, None, junk)
+    host = np.full(bh * sq * d, 7.0, np.float32)
+    fa.flash_attention_multihead_lp(fa.DTYPE_BF16, q16, k16, v16, 1, bh, sq, sk, d, None, host)
+    t16 = [torch.from_numpy(a.view(np.int16)).to(dev) for a in (q16, k16, v16)]
+    out = torch.zeros(bh * sq * d, device=dev)
+    fa.attention_device_lp(fa.DTYPE_BF16, t16[0].data_ptr(), t16[1].data_ptr(), t16[2].data_ptr(), 1, bh, sq, sk,
+                           d, False, out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(host, out.cpu().numpy())
+    assert not np.array_equal(host, junk)
+
+
 def test_split_workspace_per_stream_and_graph_replay():
     """Split partials live in a workspace kept per stream: calls queued on two
     streams without synchronising in between must not share it, a later call
