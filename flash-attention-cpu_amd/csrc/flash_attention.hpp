@@ -128,15 +128,15 @@ inline void naive_attention(Slice q, Slice k, Slice v, std::size_t seq_len_q, st
     detail::check(fa_naive_attention(q.data, q.size, k.data, k.size, v.data, v.size, seq_len_q, seq_len_k, d_head,
                                      causal ? 1 : 0, out.data, out.size));
 }
-// Aliases -- src/lib.rs:86-87
+// Aliases of v2 -- src/lib.rs:86-87 (through the C ABI's own aliases)
 inline void flash_attention(Slice q, Slice k, Slice v, std::size_t seq_len_q, std::size_t seq_len_k,
                             std::size_t d_head, const FlashAttentionConfig& config, MutSlice out) {
-    flash_attention_v2(q, k, v, seq_len_q, seq_len_k, d_head, config, out);
+    detail::single(fa_attention, q, k, v, seq_len_q, seq_len_k, d_head, config, out);
 }
 inline void flash_attention_multihead(Slice q, Slice k, Slice v, std::size_t batch, std::size_t heads,
                                       std::size_t seq_len_q, std::size_t seq_len_k, std::size_t d_head,
                                       const FlashAttentionConfig& config, MutSlice out) {
-    flash_attention_multihead_v2(q, k, v, batch, heads, seq_len_q, seq_len_k, d_head, config, out);
+    detail::multi(fa_attention_multihead, q, k, v, batch, heads, seq_len_q, seq_len_k, d_head, config, out);
 }
 
 }  // namespace flash_attention

@@ -255,9 +255,14 @@ def flash_attention_multihead_v3(q, k, v, batch, heads, seq_len_q, seq_len_k, d_
     _multi("fa_multihead_v3", q, k, v, batch, heads, seq_len_q, seq_len_k, d_head, config, out)
 
 
-# Backward-compatible aliases (src/lib.rs:86-87).
-flash_attention = flash_attention_v2
-flash_attention_multihead = flash_attention_multihead_v2
+def flash_attention(q, k, v, seq_len_q, seq_len_k, d_head, config, out) -> None:
+    """flash_attention (src/lib.rs:87): the v2 alias, through the C ABI's fa_attention."""
+    _single("fa_attention", q, k, v, seq_len_q, seq_len_k, d_head, config, out)
+
+
+def flash_attention_multihead(q, k, v, batch, heads, seq_len_q, seq_len_k, d_head, config, out) -> None:
+    """flash_attention_multihead (src/lib.rs:86): the v2 alias, through fa_attention_multihead."""
+    _multi("fa_attention_multihead", q, k, v, batch, heads, seq_len_q, seq_len_k, d_head, config, out)
 
 VARIANTS = {1: flash_attention_v1, 2: flash_attention_v2, 3: flash_attention_v3}
 MULTIHEAD_VARIANTS = {1: flash_attention_multihead_v1, 2: flash_attention_multihead_v2,
