@@ -21,6 +21,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HSACO = os.path.join(HERE, "fa_kernels.hsaco")
 LIB = os.path.join(HERE, "libfa_hip.so")
+BUILD = os.path.join(HERE, "_build")   # intermediate objects (git-ignored)
 
 # -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32.
 HIP_FLAGS = [
@@ -41,9 +42,16 @@ def build_kernels() -> str:
 
 
 def build_host() -> str:
+    """libfa_hip.so: fa_host.cpp (host-only C++) plus fa_scratch.hip, whose
+    object carries the device-global scratch array of the allocation-free
+    entry point in an embedded gfx950 code object."""
+    os.makedirs(BUILD, exist_ok=True)
+    scratch_obj = os.path.join(BUILD, "fa_scratch.o")
+    _run([os.path.join(ROCM, "bin", "hipcc"), *HIP_FLAGS, "-fPIC", "-Wall", "-Wextra", "-c",
+          os.path.join(CSRC, "fa_scratch.hip"), "-o", scratch_obj])
     _run([os.path.join(ROCM, "llvm", "bin", "clang++"), "-D__HIP_PLATFORM_AMD__",
           "-I", os.path.join(ROCM, "include"), "-fPIC", "-shared", "-O2", "-std=c++17",
-          "-Wall", "-Wextra", os.path.join(CSRC, "fa_host.cpp"),
+          "-Wall", "-Wextra", os.path.join(CSRC, "fa_host.cpp"), scratch_obj,
           "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-Wl,-rpath," + os.path.join(ROCM, "lib"),
           "-o", LIB])
     return LIB

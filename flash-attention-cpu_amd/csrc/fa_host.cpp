@@ -32,6 +32,7 @@
 #include "../../include/fa_hip.h"
 #include "fa_copy_parts.h"
 #include "fa_params.h"
+#include "fa_scratch.h"
 
 namespace {
 
@@ -210,6 +211,9 @@ int ensure_loaded(int dev) {
         hipDeviceProp_t prop;
         if (hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0)
             s.num_cus = prop.multiProcessorCount;
+        // Device address of the allocation-free entry point's scratch array;
+        // a failure here concerns only that entry point (FA_ERR_SCRATCH).
+        (void)fa_scratch_init(dev);
         s.status = FA_OK;
     });
     return s.status;
@@ -551,11 +555,16 @@ int wide_head_status(int variant, const fa_launch_opts* opts) {
     return FA_OK;
 }
 
-// Queue one attention call on device pointers.
+// Queue one attention call on device pointers.  noalloc: the split
+// partials go to the device-global scratch array (fa_scratch.hip) and the
+// call allocates nothing; plans needing more than it holds, and the naive
+// wide-head path, are refused.
 int run_device(int variant, hipStream_t stream, const void* q, const void* k, const void* v, size_t bh,
-               size_t sq, size_t sk, size_t d, int causal, const fa_launch_opts* opts, float* out) {
+               size_t sq, size_t sk, size_t d, int causal, const fa_launch_opts* opts, float* out,
+               bool noalloc = false) {
     if (bh == 0 || sq == 0 || sk == 0 || d == 0) return FA_OK;   // src/common.rs:56
     if (!q || !k || !v || !out) return FA_ERR_INVALID_ARG;
+    if (d > (size_t)kMaxD && noalloc) return FA_ERR_UNSUPPORTED;
     if (d > (size_t)kMaxD) {
         const int rc = wide_head_status(variant, opts);
         if (rc != FA_OK) return rc;
@@ -575,8 +584,11 @@ int run_device(int variant, hipStream_t stream, const void* q, const void* k, co
 
     const size_t bytes = plan.ws_floats * sizeof(float);
     float* ws = nullptr;
-    const bool cached = bytes <= kWorkspaceCacheMax;
-    if (cached) {
+    const bool cached = noalloc || bytes <= kWorkspaceCacheMax;
+    if (noalloc) {
+        ws = static_cast<float*>(fa_scratch_ptr(dev));
+        if (!ws || bytes > FA_SCRATCH_BYTES) return FA_ERR_SCRATCH;
+    } else if (cached) {
         rc = stream_workspace(dev, stream, bytes, reinterpret_cast<void**>(&ws));
         if (rc != FA_OK) return rc;
     } else if (hipMallocAsync(reinterpret_cast<void**>(&ws), bytes, stream) != hipSuccess) {
@@ -890,6 +902,7 @@ const char* fa_status_string(int status) {
         case FA_ERR_ALLOC: return "device allocation failed";
         case FA_ERR_LAUNCH: return "kernel launch failed";
         case FA_ERR_COPY: return "host/device copy failed";
+        case FA_ERR_SCRATCH: return "split workspace larger than the 64 MiB no-alloc scratch, or scratch unavailable";
         default: return "unknown status";
     }
 }
@@ -993,6 +1006,15 @@ int fa_device_ex(int variant, void* stream, const float* q, const float* k, cons
                       cfg ? cfg->causal : 0, opts, out);
 }
 
+int fa_device_ex_noalloc(int variant, void* stream, const float* q, const float* k, const float* v, size_t batch,
+                         size_t heads, size_t sq, size_t sk, size_t d, const fa_config* cfg,
+                         const fa_launch_opts* opts, float* out) {
+    if (variant < 1 || variant > 3) return FA_ERR_INVALID_ARG;
+    if (opts && opts->dtype != FA_DTYPE_F32) return FA_ERR_INVALID_ARG;
+    return run_device(variant, static_cast<hipStream_t>(stream), q, k, v, batch * heads, sq, sk, d,
+                      cfg ? cfg->causal : 0, opts, out, /*noalloc=*/true);
+}
+
 int fa_device_lp(int dtype, void* stream, const void* q, const void* k, const void* v, size_t batch, size_t heads,
                  size_t sq, size_t sk, size_t d, const fa_config* cfg, const fa_launch_opts* opts, float* out) {
     if (dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F16) return FA_ERR_INVALID_ARG;
@@ -1063,6 +1085,8 @@ int fa_describe_launch(int variant, size_t batch, size_t heads, size_t sq, size_
                     std::snprintf(tmp, sizeof(tmp), " split_len=%d", plan.p.split_len);
                     text += tmp;
                 }
+                std::snprintf(tmp, sizeof(tmp), " workspace=%zu", plan.ws_floats * sizeof(float));
+                text += tmp;
             }
         }
     }

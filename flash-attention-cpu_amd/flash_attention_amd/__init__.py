@@ -45,6 +45,7 @@ FA_ERR_MODULE = 8
 FA_ERR_ALLOC = 9
 FA_ERR_LAUNCH = 10
 FA_ERR_COPY = 11
+FA_ERR_SCRATCH = 12
 
 PATH_AUTO = 0
 PATH_PREFILL = 1
@@ -63,7 +64,7 @@ EXPORTED_SYMBOLS = (
     "fa_status_string", "fa_config_default",
     "fa_v1", "fa_v2", "fa_v3", "fa_attention",
     "fa_multihead_v1", "fa_multihead_v2", "fa_multihead_v3", "fa_attention_multihead",
-    "fa_device_v1", "fa_device_v2", "fa_device_v3", "fa_device_ex",
+    "fa_device_v1", "fa_device_v2", "fa_device_v3", "fa_device_ex", "fa_device_ex_noalloc",
     "fa_device_lp", "fa_multihead_lp",
     "fa_naive_attention", "fa_naive_device",
     "fa_init", "fa_describe_launch",
@@ -152,6 +153,8 @@ def lib() -> ctypes.CDLL:
     L.fa_device_ex.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                ctypes.c_void_p, _SZ, _SZ, _SZ, _SZ, _SZ, _CFG, _OPTS, ctypes.c_void_p]
     L.fa_device_ex.restype = ctypes.c_int
+    L.fa_device_ex_noalloc.argtypes = L.fa_device_ex.argtypes
+    L.fa_device_ex_noalloc.restype = ctypes.c_int
     L.fa_device_lp.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                _SZ, _SZ, _SZ, _SZ, _SZ, _CFG, _OPTS, ctypes.c_void_p]
     L.fa_device_lp.restype = ctypes.c_int
@@ -345,6 +348,20 @@ def attention_device(variant: int, q_ptr: int, k_ptr: int, v_ptr: int, batch: in
                               ctypes.c_void_p(k_ptr), ctypes.c_void_p(v_ptr), batch, heads, seq_len_q,
                               seq_len_k, d_head, ctypes.byref(cfg), ctypes.byref(opts),
                               ctypes.c_void_p(out_ptr)))
+
+
+def attention_device_noalloc(variant: int, q_ptr: int, k_ptr: int, v_ptr: int, batch: int, heads: int,
+                             seq_len_q: int, seq_len_k: int, d_head: int, causal: bool, out_ptr: int,
+                             stream: int = 0, softmax_scale: float | None = None, path: int = PATH_AUTO,
+                             num_splits: int = 0) -> None:
+    """As attention_device, through fa_device_ex_noalloc: split partials in the
+    library's device-global scratch array, no device allocation."""
+    cfg = _CConfig(64, 128, 1 if causal else 0)
+    opts = _COpts(float(softmax_scale) if softmax_scale else 0.0, int(path), int(num_splits))
+    _check(lib().fa_device_ex_noalloc(int(variant), ctypes.c_void_p(stream), ctypes.c_void_p(q_ptr),
+                                      ctypes.c_void_p(k_ptr), ctypes.c_void_p(v_ptr), batch, heads, seq_len_q,
+                                      seq_len_k, d_head, ctypes.byref(cfg), ctypes.byref(opts),
+                                      ctypes.c_void_p(out_ptr)))
 
 
 def describe_launch(variant: int, batch: int, heads: int, seq_len_q: int, seq_len_k: int, d_head: int,

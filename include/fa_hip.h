@@ -45,6 +45,8 @@ extern "C" {
 #define FA_ERR_ALLOC 9        /* device allocation failed */
 #define FA_ERR_LAUNCH 10      /* kernel launch failed */
 #define FA_ERR_COPY 11        /* host<->device copy or synchronisation failed */
+#define FA_ERR_SCRATCH 12     /* fa_device_ex_noalloc: the call needs more split workspace than
+                                 the 64 MiB scratch array, or the array is unavailable */
 
 /* Human-readable text for a status code (static storage). */
 const char* fa_status_string(int status);
@@ -168,6 +170,23 @@ typedef struct fa_launch_opts {
 int fa_device_ex(int variant, void* stream, const float* q, const float* k, const float* v,
                  size_t batch, size_t heads, size_t seq_len_q, size_t seq_len_k, size_t d_head,
                  const fa_config* config, const fa_launch_opts* opts, float* out);
+
+/* ---- allocation-free form ------------------------------------------------
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  Same arguments, kernels and results as fa_device_ex,
+ * but the split partials (split-KV decode, prefill key split) go to a
+ * device-global scratch array of 64 MiB per GPU, held until the process
+ * ends, and the call allocates and frees nothing.  Calls whose plan needs a
+ * larger workspace return FA_ERR_SCRATCH (out untouched); d_head > 256 (the
+ * naive kernels' score matrix) returns FA_ERR_UNSUPPORTED.  Call fa_init()
+ * on each device first (it loads the kernels and maps the array; a first
+ * call does it itself, which allocates).  All calls on one GPU share its
+ * array: calls that may overlap on one GPU (different streams, or graphs
+ * replayed concurrently) race on it and must be ordered by the caller. */
+int fa_device_ex_noalloc(int variant, void* stream, const float* q, const float* k, const float* v,
+                         size_t batch, size_t heads, size_t seq_len_q, size_t seq_len_k, size_t d_head,
+                         const fa_config* config, const fa_launch_opts* opts, float* out);
 
 /* ---- 16-bit inputs (bf16 / f16) -------------------------------------------
  * Not in the reference, whose roadmap plans bf16 dot products with f32

@@ -63,7 +63,7 @@ def test_status_strings():
     assert fa.status_string(fa.FA_ERR_K_SHAPE) == "k shape mismatch"
     assert fa.status_string(fa.FA_ERR_V_SHAPE) == "v shape mismatch"
     assert fa.status_string(fa.FA_ERR_OUT_SHAPE) == "out shape mismatch"
-    for code in range(5, 12):
+    for code in range(5, 13):
         assert fa.status_string(code) not in ("ok", "unknown status")
     assert fa.status_string(999) == "unknown status"
 
@@ -239,7 +239,7 @@ def test_planning_key_split_prefill():
     # config 5c: 8 query blocks x 16 heads = 128 workgroups < 256 CUs
     s = describe(3, 1, 16, 1000, 1000, 256, True)
     assert s.startswith("fa_prefill_v3_d256_2 grid=") and "fa_merge_d256 grid=16000x1x1" in s
-    nks, split_len = int(s.split("splits=")[1].split()[0]), int(s.split("split_len=")[1])
+    nks, split_len = int(s.split("splits=")[1].split()[0]), int(s.split("split_len=")[1].split()[0])
     assert split_len % 16 == 0 and nks * split_len >= 1000 > (nks - 1) * split_len
     # compact grid: split y of every 128-row block whose causal key end passes y * split_len
     wgs = 16 * sum(1 for y in range(nks) for qb in range(8) if min(1000, 128 * (qb + 1)) > y * split_len)
