@@ -1,20 +1,29 @@
 #!/usr/bin/env python3
-"""Benchmark: FlashAttention forward on one MI355X.
+"""Benchmark: FlashAttention forward on one MI355X, every configuration.
 
-Headline (BASELINE.json metric, configs[1]): 32 heads x 2048 x 2048, d_head
-128, causal, f32, inputs resident in HBM.  A "step" is one attention call
-over that batch.  ``value`` is whole-job TFLOP/s (algorithmic FLOP
+Headline (the metric's configuration): 32 heads x 2048 x 2048, d_head 128,
+causal, f32, v3, inputs resident in HBM.  A "step" is one attention call over
+that batch.  ``value`` is whole-job TFLOP/s (algorithmic FLOP
 4*d*visible_pairs*heads over wall time between synchronisations); the
 ``roofline`` object prices the prefill kernel's own duration (HIP events on
-the launch stream) against the FP32-MFMA peak.  Decode shapes
-are reported in ``extra`` as GB/s against the 8 TB/s HBM peak.
+the launch stream) against the FP32-MFMA peak, and ``roofline.traffic`` is
+the kernel's measured HBM bytes per launch (rocprofv3 counters, reported only
+while the kernel sources match the ones profiled).
 
-``cpu_baseline`` times the CPU oracle's v2 (oracle/, a C restatement of the
-reference crate's rayon + AVX-512/AVX2 path, src/v2.rs:160-385) on the same
-inputs, on the host cores, as a reported baseline only.
+Every other configuration (1, 3, 4a, 4b, 5, 5c; v1/v2/v3) is timed the same
+way into ``extra.configs`` -- TFLOP/s and % of the FP32-MFMA peak for
+prefill shapes, GB/s and % of 8 TB/s for decode shapes -- next to a CPU
+baseline on the same inputs: the oracle's v2 (oracle/, a C restatement of the
+reference crate's rayon + AVX-512/AVX2 path, src/v2.rs:160-385) on all host
+cores, time-boxed, ms/call and GFLOP/s (GB/s for decode) as
+examples/bench_quick.rs:13-21 reports them.  The CPU v2 output is also the
+parity reference: every GPU output timed here is compared with it (max-abs,
+relative L2; north_star bar 2e-5 / 1e-5), and the headline's figures are the
+top-level ``parity`` object.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--variant 3]
-                       [--all] [--no-cpu-baseline]
+                       [--quick | --configs config2,config4a,...]
+                       [--no-cpu-baseline] [--cpu-seconds S]
 Prints exactly one JSON line on stdout; progress goes to stderr.
 """
 from __future__ import annotations
@@ -32,6 +41,19 @@ METRIC = "attention TFLOP/s f32 (32h×2048×d128 causal) + % FP32-MFMA peak; dec
 PEAK_TFLOPS = 157.3     # MI355X dense FP32 MFMA
 PEAK_GBS = 8000.0       # MI355X HBM3E
 PEAK_TFLOPS_16 = 2500.0  # MI355X dense bf16 / f16 MFMA
+MAX_ABS_TOL, REL_L2_TOL = 2e-5, 1e-5   # north_star parity bar against CPU v2
+
+# name, heads, seq_q, seq_k, d_head, causal, Q/K std, V ~ U(-1, 1), kind
+CONFIGS = [
+    ("config1", 1, 256, 256, 64, False, 1.0, False, "prefill"),
+    ("config2", 32, 2048, 2048, 128, True, 1.0, False, "prefill"),
+    ("config3", 8, 16384, 16384, 128, True, 1.0, False, "prefill"),
+    ("config4a", 32, 1, 32768, 128, False, 1.0, False, "decode"),
+    ("config4b", 32, 16, 32768, 128, False, 1.0, False, "decode"),
+    ("config5", 16, 4096, 1024, 256, False, 3.0, True, "prefill"),
+    ("config5c", 16, 1000, 1000, 256, True, 3.0, True, "prefill"),
+]
+HEADLINE = "config2"
 
 
 def log(msg: str) -> None:
@@ -55,8 +77,9 @@ def bytes_of(bh, sq, sk, d) -> int:
 
 
 class Workload:
-    def __init__(self, torch, name, bh, sq, sk, d, causal, qk_sigma=1.0, v_uniform=False):
+    def __init__(self, torch, name, bh, sq, sk, d, causal, qk_sigma=1.0, v_uniform=False, kind="prefill"):
         self.name, self.bh, self.sq, self.sk, self.d, self.causal = name, bh, sq, sk, d, causal
+        self.kind = kind
         dev = torch.device("cuda", 0)
         gens = []
         for seed in (1, 2, 3):   # seeds Q=1, K=2, V=3
@@ -73,25 +96,24 @@ class Workload:
         self.flops = flops_of(bh, sq, sk, d, causal)
         self.bytes = bytes_of(bh, sq, sk, d)
 
+    def describe(self):
+        dist = "N(0,1)" if self.kind == "decode" or self.d != 256 else "Q,K ~ N(0,3^2), V ~ U(-1,1)"
+        return (f"{self.name}: {self.bh}h x {self.sq} x {self.sk}, d{self.d}, "
+                f"{'causal' if self.causal else 'non-causal'}, {dist}")
+
 
 RAMP_SECONDS = 0.3   # untimed sustained work before each measurement (clock ramp)
 
 
-def time_steps(torch, fa, wl: Workload, variant: int, steps: int, warmup: int):
+def time_calls(torch, call, steps: int, warmup: int):
     """Clock ramp, W warm-up calls, then K timed calls between synchronisations.
 
     An MI355X coming out of idle runs its first ~10-20 ms of work at a lower
     clock (measured: the first calls of a run are 10-15 % slower than the
     steady state), so every measurement first repeats the same call, untimed,
     for RAMP_SECONDS.  Returns (wall ms per step, kernel-stream ms per step
-    from HIP events)."""
+    from HIP events on the launch stream)."""
     stream = torch.cuda.current_stream()
-    handle = stream.cuda_stream
-
-    def call():
-        fa.attention_device(variant, wl.q.data_ptr(), wl.k.data_ptr(), wl.v.data_ptr(), 1, wl.bh, wl.sq,
-                            wl.sk, wl.d, wl.causal, wl.o.data_ptr(), handle)
-
     t_ramp = time.perf_counter()
     while True:
         for _ in range(8):
@@ -114,6 +136,26 @@ def time_steps(torch, fa, wl: Workload, variant: int, steps: int, warmup: int):
     return (t1 - t0) * 1e3 / steps, e0.elapsed_time(e1) / steps
 
 
+def f32_call(torch, fa, wl: Workload, variant: int):
+    handle = torch.cuda.current_stream().cuda_stream
+
+    def call():
+        fa.attention_device(variant, wl.q.data_ptr(), wl.k.data_ptr(), wl.v.data_ptr(), 1, wl.bh, wl.sq,
+                            wl.sk, wl.d, wl.causal, wl.o.data_ptr(), handle)
+    return call
+
+
+def auto_steps(torch, call, cap: int, target_ms: float = 40.0) -> int:
+    """Timed calls for about target_ms of GPU time (at least 3, at most cap)."""
+    call()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    call()
+    torch.cuda.synchronize()
+    one = (time.perf_counter() - t0) * 1e3
+    return int(max(3, min(cap, target_ms / max(one, 1e-3))))
+
+
 def time_host_slice(fa, wl: Workload, variant: int, calls: int) -> float:
     """The drop-in host-slice call (fa_multihead_vN: copy in, run, copy out),
     ms per call after one warm-up.  PCIe-inclusive; never the headline."""
@@ -130,57 +172,60 @@ def time_host_slice(fa, wl: Workload, variant: int, calls: int) -> float:
     return (time.perf_counter() - t0) * 1e3 / calls
 
 
-def read_traffic(kernel: str, workload: str):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
-    path = os.path.join(ROOT, "profiles", "traffic.json")
+def grid_threads(describe: str) -> int:
+    """Threads in the first launch of a fa_describe_launch string ("name grid=AxBxC block=T ...")."""
+    first = describe.split(";")[0].split()
+    g = [int(x) for x in first[1].split("=")[1].split("x")]
+    return g[0] * g[1] * g[2] * int(first[2].split("=")[1])
+
+
+def host_cores() -> int:
     try:
-        with open(path) as f:
-            table = json.load(f)
-    except (OSError, ValueError):
-        return None
-    ent = table.get(kernel)
-    if not ent or ent.get("workload") != workload:
-        return None
-    return ent.get("hbm_bytes_per_launch")
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
 
 
-def cpu_baseline(wl: Workload, budget_s: float):
-    """Oracle v2 (C restatement of the crate's CPU v2) on the same inputs."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle   # test infrastructure: the timed CPU baseline only
-
-    q = wl.q.cpu().numpy()
-    k = wl.k.cpu().numpy()
-    v = wl.v.cpu().numpy()
-    threads = min(16, os.cpu_count() or 1)
-    tier = oracle.best_tier()
-    oracle.run(2, q, k, v, wl.bh, wl.sq, wl.sk, wl.d, wl.causal, 64, 128, nthreads=threads)   # warm-up
-    n, t0 = 0, time.perf_counter()
-    while True:
-        oracle.run(2, q, k, v, wl.bh, wl.sq, wl.sk, wl.d, wl.causal, 64, 128, nthreads=threads)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or n >= 200:
-            break
-    per_call = el / n
-    model = "unknown CPU"
+def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
                 if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
+                    return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {
-        "value": round(wl.flops / per_call / 1e12, 4),
-        "unit": "TFLOP/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"{wl.name}: full workload ({wl.bh} heads), {n} calls after 1 warm-up, "
-                   f"{per_call * 1e3:.1f} ms/call, oracle v2 {oracle.TIER_NAMES[tier]} tier, "
-                   f"Br=64 Bc=128, {threads} threads on {model} ({os.cpu_count()} logical CPUs visible)"),
-    }
+    return "unknown CPU"
+
+
+def cpu_v2(inputs, wl: Workload, budget_s: float, threads: int):
+    """Oracle v2 (C restatement of the crate's CPU v2) on the same inputs:
+    one warm-up call, then calls until budget_s (at least one).  Returns
+    (output of the last call, seconds per call, calls)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle   # test infrastructure: the timed CPU baseline and the checker only
+
+    q, k, v = inputs
+    out = oracle.run(2, q, k, v, wl.bh, wl.sq, wl.sk, wl.d, wl.causal, 64, 128, nthreads=threads)   # warm-up
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oracle.run(2, q, k, v, wl.bh, wl.sq, wl.sk, wl.d, wl.causal, 64, 128, nthreads=threads, out=out)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 200:
+            break
+    return out, el / n, n
+
+
+def parity(got, want) -> dict:
+    import numpy as np
+
+    g = np.asarray(got, np.float64)
+    w = np.asarray(want, np.float64)
+    ma = float(np.max(np.abs(g - w))) if g.size else 0.0
+    den = float(np.linalg.norm(w))
+    rl = float(np.linalg.norm(g - w)) / (den if den > 0 else 1.0)
+    return {"max_abs": float(f"{ma:.3g}"), "rel_l2": float(f"{rl:.3g}"),
+            "within_bar": bool(np.all(np.isfinite(g)) and ma < MAX_ABS_TOL and rl < REL_L2_TOL)}
 
 
 def main() -> int:
@@ -189,12 +234,15 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--variant", type=int, default=3, choices=(1, 2, 3))
-    ap.add_argument("--all", action="store_true", help="also time configs 1, 3, 5, 5c")
+    ap.add_argument("--quick", "--only-config2", action="store_true", dest="quick",
+                    help="time only the headline workload's f32 variants (profiling runs)")
+    ap.add_argument("--configs", default="",
+                    help="comma-separated subset of " + ",".join(c[0] for c in CONFIGS) + " (the headline always runs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU budget of the headline baseline")
+    ap.add_argument("--cpu-seconds-other", type=float, default=2.5, help="CPU budget of each other config")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="only run 5 plain device copies of N MiB (rocprofv3 PMC scale reference) and exit")
-    ap.add_argument("--only-config2", action="store_true", help="time only the headline workload")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -204,6 +252,7 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
+    import numpy as np
     import torch
 
     if args.calibrate_copy_mib:
@@ -217,122 +266,106 @@ def main() -> int:
         return 0
 
     import flash_attention_amd as fa
+    from flash_attention_amd.traffic import kernel_source_hash, lookup
 
     fa.init()
-    extra = {}
+    traffic_table = os.path.join(ROOT, "profiles", "traffic.json")
+    configs = {}
+    pending_cpu = []   # (name, workload, host inputs, {variant: GPU output})
+    result_head = None
 
-    head = Workload(torch, "config2: 32h x 2048 x 2048, d128, causal, N(0,1)", 32, 2048, 2048, 128, True)
-    kernel = fa.describe_launch(args.variant, 1, head.bh, head.sq, head.sk, head.d, head.causal).split()[0]
-    ms_step, ms_kernel = time_steps(torch, fa, head, args.variant, args.steps, args.warmup)
-    value = head.flops / (ms_step * 1e-3) / 1e12
-    achieved = head.flops / (ms_kernel * 1e-3) / 1e12
-    log(f"[bench] config2 v{args.variant}: {ms_step * 1e3:.1f} us/step wall, {ms_kernel * 1e3:.1f} us kernel, "
-        f"{value:.2f} TFLOP/s")
-
-    if not args.only_config2:
-        # The survey's protocol: R = 5 repeats of 20 launches, median us/call.
-        reps = sorted(time_steps(torch, fa, head, args.variant, 20, 3)[1] for _ in range(5))
-        extra[f"config2_v{args.variant}_median_5x20_us"] = round(reps[2] * 1e3, 1)
-        log(f"[bench] config2 v{args.variant}: median of 5 x 20 launches {reps[2] * 1e3:.1f} us")
-    for var in (() if args.only_config2 else (1, 2, 3)):
-        if var == args.variant:
-            m_w, m_k = ms_step, ms_kernel
-        else:
-            m_w, m_k = time_steps(torch, fa, head, var, max(5, args.steps // 2), args.warmup)
-        extra[f"config2_v{var}"] = {"us_per_call": round(m_k * 1e3, 1),
-                                    "tflops": round(head.flops / (m_k * 1e-3) / 1e12, 2),
-                                    "pct_fp32_mfma_peak": round(100 * head.flops / (m_k * 1e-3) / 1e12
-                                                                / PEAK_TFLOPS, 1)}
-        log(f"[bench] config2 v{var}: {m_k * 1e3:.1f} us, {extra[f'config2_v{var}']['tflops']} TFLOP/s")
-    if not args.only_config2:
-        ms = time_host_slice(fa, head, args.variant, 5)
-        extra[f"config2_host_slice_v{args.variant}"] = {"ms_per_call": round(ms, 3),
-                                                        "tflops_incl_pcie": round(head.flops / (ms * 1e-3) / 1e12, 2)}
-        log(f"[bench] config2 host-slice v{args.variant}: {ms:.2f} ms/call incl. PCIe copies")
-
-    # Decode shapes: split-KV + merge, bandwidth-bound.
-    k_dec = v_dec = None
-    for sq in (() if args.only_config2 else (1, 16)):
-        wl = Workload(torch, f"config4 seq_q={sq}", 32, sq, 32768, 128, False)
-        if k_dec is not None:   # share K/V (1 GiB) between the two decode shapes
-            wl.k, wl.v = k_dec, v_dec
-        k_dec, v_dec = wl.k, wl.v
-        _, m_k = time_steps(torch, fa, wl, 2, max(10, args.steps), args.warmup)
-        gbs = wl.bytes / (m_k * 1e-3) / 1e9
-        extra[f"config4_decode_sq{sq}"] = {"us_per_call": round(m_k * 1e3, 1), "gbs": round(gbs, 1),
-                                           "pct_hbm_peak": round(100 * gbs / PEAK_GBS, 1),
-                                           "kernels": fa.describe_launch(2, 1, 32, sq, 32768, 128, False)}
-        log(f"[bench] config4 seq_q={sq}: {m_k * 1e3:.1f} us, {gbs:.0f} GB/s")
-        if sq == 1:
-            ms = time_host_slice(fa, wl, 2, 2)
-            extra["config4_host_slice_sq1"] = {"ms_per_call": round(ms, 2),
-                                               "gbs_incl_pcie": round(wl.bytes / (ms * 1e-3) / 1e9, 1)}
-            log(f"[bench] config4 seq_q=1 host-slice: {ms:.1f} ms/call incl. PCIe copies")
-        del wl
-    del k_dec, v_dec
-    torch.cuda.empty_cache()
-
-    # 16-bit inputs (fa_device_lp): config 2 and the decode shape, same seeds,
-    # rounded to bf16 / f16; FLOP against the 16-bit MFMA peak, bytes at 2 B.
-    for name, dt, tdt in ((() if args.only_config2 else (("bf16", fa.DTYPE_BF16, torch.bfloat16),
-                                                          ("f16", fa.DTYPE_F16, torch.float16)))):
-        for tag, wl in (("config2", head), ("config4_decode_sq1", None)):
-            if wl is None:
-                wl = Workload(torch, "config4 seq_q=1", 32, 1, 32768, 128, False)
-            lq, lk, lv = wl.q.to(tdt), wl.k.to(tdt), wl.v.to(tdt)
-            stream = torch.cuda.current_stream()
-
-            def call_lp():
-                fa.attention_device_lp(dt, lq.data_ptr(), lk.data_ptr(), lv.data_ptr(), 1, wl.bh, wl.sq, wl.sk,
-                                       wl.d, wl.causal, wl.o.data_ptr(), stream.cuda_stream)
-
-            t_ramp = time.perf_counter()
-            while time.perf_counter() - t_ramp < RAMP_SECONDS:
-                for _ in range(8):
-                    call_lp()
-                torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            n = max(10, args.steps)
-            e0.record(stream)
-            for _ in range(n):
-                call_lp()
-            e1.record(stream)
-            torch.cuda.synchronize()
-            ms = e0.elapsed_time(e1) / n
-            ent = {"us_per_call": round(ms * 1e3, 1),
-                   "kernels": fa.describe_launch(3, 1, wl.bh, wl.sq, wl.sk, wl.d, wl.causal, dtype=dt)}
-            if tag == "config2":
-                tf = wl.flops / (ms * 1e-3) / 1e12
-                ent.update(tflops=round(tf, 1), pct_16bit_mfma_peak=round(100 * tf / PEAK_TFLOPS_16, 1))
+    chosen = {c for c in args.configs.split(",") if c}
+    unknown = chosen - {c[0] for c in CONFIGS}
+    if unknown:
+        print(f"bench.py: unknown config(s) {sorted(unknown)}", file=sys.stderr)
+        return 2
+    for (name, bh, sq, sk, d, causal, sig, vu, kind) in CONFIGS:
+        if name != HEADLINE and (args.quick or (chosen and name not in chosen)):
+            continue
+        wl = Workload(torch, name, bh, sq, sk, d, causal, sig, vu, kind)
+        entry = {"shape": wl.describe(), "algorithmic_flop": wl.flops, "algorithmic_bytes": wl.bytes}
+        outs = {}
+        variants = (1, 2, 3)
+        if name == HEADLINE:   # the headline variant first, with the requested step counts
+            variants = (args.variant,) + tuple(x for x in (1, 2, 3) if x != args.variant)
+        for var in variants:
+            call = f32_call(torch, fa, wl, var)
+            kernels = fa.describe_launch(var, 1, bh, sq, sk, d, causal)
+            if name == HEADLINE and var == args.variant:
+                ms_step, ms_kernel = time_calls(torch, call, args.steps, args.warmup)
+                result_head = (wl, kernels, ms_step, ms_kernel)
+                log(f"[bench] {name} v{var}: {ms_step * 1e3:.1f} us/step wall, {ms_kernel * 1e3:.1f} us kernel")
+                if not args.quick:
+                    # The survey's protocol: R = 5 repeats of 20 launches, median us/call.
+                    reps = sorted(time_calls(torch, call, 20, 3)[1] for _ in range(5))
+                    entry[f"v{var}_median_5x20_us"] = round(reps[2] * 1e3, 1)
             else:
-                lp_bytes = wl.bh * wl.d * (2 * wl.sq + 4 * wl.sk + 4 * wl.sq)   # 16-bit Q, K, V; f32 O
-                gbs = lp_bytes / (ms * 1e-3) / 1e9
+                steps = auto_steps(torch, call, max(5, args.steps))
+                _, ms_kernel = time_calls(torch, call, steps, 2)
+            torch.cuda.synchronize()
+            outs[var] = wl.o.cpu().numpy().copy()
+            ent = {"us_per_call": round(ms_kernel * 1e3, 1), "kernels": kernels}
+            tf = wl.flops / (ms_kernel * 1e-3) / 1e12
+            ent["tflops"] = round(tf, 2)
+            if kind == "prefill":
+                ent["pct_fp32_mfma_peak"] = round(100 * tf / PEAK_TFLOPS, 1)
+            else:
+                gbs = wl.bytes / (ms_kernel * 1e-3) / 1e9
                 ent.update(gbs=round(gbs, 1), pct_hbm_peak=round(100 * gbs / PEAK_GBS, 1))
-            extra[f"{tag}_{name}"] = ent
-            log(f"[bench] {tag} {name}: {ent}")
-            del lq, lk, lv
-            if tag != "config2":
-                del wl
+            tb, why = lookup(traffic_table, kernels.split()[0], grid_threads(kernels))
+            if tb is not None:
+                ent["hbm_bytes_per_launch"] = tb
+            entry[f"v{var}"] = ent
+            log(f"[bench] {name} v{var}: {ent}")
+        if not args.quick and name in ("config2", "config4a"):
+            var = args.variant if name == HEADLINE else 2
+            ms = time_host_slice(fa, wl, var, 5 if name == "config2" else 2)
+            entry[f"host_slice_v{var}"] = {"ms_per_call": round(ms, 3),
+                                           "tflops_incl_pcie": round(wl.flops / (ms * 1e-3) / 1e12, 3),
+                                           "gbs_incl_pcie": round(wl.bytes / (ms * 1e-3) / 1e9, 1)}
+            log(f"[bench] {name} host-slice v{var}: {ms:.2f} ms/call incl. PCIe copies")
+        if not args.quick:
+            for tname, dt, tdt in (("bf16", fa.DTYPE_BF16, torch.bfloat16), ("f16", fa.DTYPE_F16, torch.float16)):
+                if name not in ("config2", "config3", "config4a", "config5"):
+                    continue
+                # 16-bit inputs (fa_device_lp): the same inputs rounded; FLOP
+                # against the 16-bit MFMA peak, bytes at 2 B per input element.
+                if name == "config3" and tname == "f16":
+                    continue
+                lq, lk, lv = wl.q.to(tdt), wl.k.to(tdt), wl.v.to(tdt)
+                handle = torch.cuda.current_stream().cuda_stream
+
+                def call_lp(lq=lq, lk=lk, lv=lv, dt=dt):
+                    fa.attention_device_lp(dt, lq.data_ptr(), lk.data_ptr(), lv.data_ptr(), 1, wl.bh, wl.sq,
+                                           wl.sk, wl.d, wl.causal, wl.o.data_ptr(), handle)
+
+                steps = auto_steps(torch, call_lp, max(10, args.steps))
+                _, ms = time_calls(torch, call_lp, steps, 2)
+                ent = {"us_per_call": round(ms * 1e3, 1),
+                       "kernels": fa.describe_launch(3, 1, wl.bh, wl.sq, wl.sk, wl.d, wl.causal, dtype=dt)}
+                if kind == "prefill":
+                    tf = wl.flops / (ms * 1e-3) / 1e12
+                    ent.update(tflops=round(tf, 1), pct_16bit_mfma_peak=round(100 * tf / PEAK_TFLOPS_16, 1))
+                else:
+                    lp_bytes = wl.bh * wl.d * (2 * wl.sq + 4 * wl.sk + 4 * wl.sq)   # 16-bit Q, K, V; f32 O
+                    gbs = lp_bytes / (ms * 1e-3) / 1e9
+                    ent.update(gbs=round(gbs, 1), pct_hbm_peak=round(100 * gbs / PEAK_GBS, 1))
+                entry[tname] = ent
+                log(f"[bench] {name} {tname}: {ent}")
+                del lq, lk, lv
+        configs[name] = entry
+        if not args.no_cpu_baseline:
+            inputs = (wl.q.cpu().numpy(), wl.k.cpu().numpy(), wl.v.cpu().numpy())
+            pending_cpu.append((name, wl, inputs, outs))
+        if name != HEADLINE:
+            wl.q = wl.k = wl.v = wl.o = None
         torch.cuda.empty_cache()
 
-    if args.all:
-        for name, shape in (("config1", (1, 256, 256, 64, False, 1.0, False)),
-                            ("config3", (8, 16384, 16384, 128, True, 1.0, False)),
-                            ("config5", (16, 4096, 1024, 256, False, 3.0, True)),
-                            ("config5c", (16, 1000, 1000, 256, True, 3.0, True))):
-            bh, sq, sk, d, causal, sig, vu = shape
-            wl = Workload(torch, name, bh, sq, sk, d, causal, sig, vu)
-            for var in (1, 2, 3):
-                steps = 3 if name == "config3" else max(5, args.steps // 2)
-                _, m_k = time_steps(torch, fa, wl, var, steps, 2)
-                tf = wl.flops / (m_k * 1e-3) / 1e12
-                extra[f"{name}_v{var}"] = {"us_per_call": round(m_k * 1e3, 1), "tflops": round(tf, 2),
-                                           "pct_fp32_mfma_peak": round(100 * tf / PEAK_TFLOPS, 1)}
-                log(f"[bench] {name} v{var}: {m_k * 1e3:.1f} us, {tf:.2f} TFLOP/s")
-            del wl
-            torch.cuda.empty_cache()
-
-    traffic = read_traffic(kernel, "config2")
+    wl, kernels, ms_step, ms_kernel = result_head
+    kernel = kernels.split()[0]
+    value = wl.flops / (ms_step * 1e-3) / 1e12
+    achieved = wl.flops / (ms_kernel * 1e-3) / 1e12
+    traffic, traffic_note = lookup(traffic_table, kernel, grid_threads(kernels))
     result = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -352,12 +385,40 @@ def main() -> int:
                    "variant": f"v{args.variant}", "kernel": kernel},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": traffic},
-        "extra": extra,
+        "extra": {"configs": configs, "traffic_note": traffic_note, "kernel_source_sha256": kernel_source_hash()},
     }
-    if not args.no_cpu_baseline:
-        log("[bench] cpu baseline ...")
-        result["cpu_baseline"] = cpu_baseline(head, args.cpu_seconds)
-        log(f"[bench] cpu baseline: {result['cpu_baseline']}")
+
+    if pending_cpu:
+        threads = host_cores()
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle
+
+        tier = oracle.TIER_NAMES[oracle.best_tier()]
+        for name, cwl, inputs, outs in pending_cpu:
+            budget = args.cpu_seconds if name == HEADLINE else args.cpu_seconds_other
+            log(f"[bench] cpu baseline {name} ({budget:.1f} s budget, {threads} threads) ...")
+            want, sec, n = cpu_v2(inputs, cwl, budget, threads)
+            ent = {"ms_per_call": round(sec * 1e3, 3), "calls": n, "threads": threads, "tier": tier,
+                   "gflops": round(cwl.flops / sec / 1e9, 2)}
+            if cwl.kind == "decode":
+                ent["gbs"] = round(cwl.bytes / sec / 1e9, 2)
+            configs[name]["cpu_v2"] = ent
+            configs[name]["parity_vs_cpu_v2"] = {f"v{var}": parity(o, want) for var, o in sorted(outs.items())}
+            log(f"[bench] {name} cpu v2: {ent}; parity {configs[name]['parity_vs_cpu_v2']}")
+            if name == HEADLINE:
+                result["cpu_baseline"] = {
+                    "value": round(cwl.flops / sec / 1e12, 4),
+                    "unit": "TFLOP/s",
+                    "cores": threads,
+                    "kind": "port",
+                    "sample": (f"{cwl.describe()}: full workload ({cwl.bh} heads), {n} calls after 1 warm-up, "
+                               f"{sec * 1e3:.1f} ms/call, oracle v2 {tier} tier, Br=64 Bc=128, {threads} threads "
+                               f"on {cpu_model()} ({threads} logical CPUs available)"),
+                }
+                p = configs[name]["parity_vs_cpu_v2"][f"v{args.variant}"]
+                result["parity"] = dict(p, vs="oracle v2 on the host, same inputs as the timed calls",
+                                        bar={"max_abs": MAX_ABS_TOL, "rel_l2": REL_L2_TOL})
+            del want
     print(json.dumps(result), flush=True)
     return 0
 
