@@ -71,10 +71,10 @@ struct DeviceState {
     struct Workspace {
         void* ptr = nullptr;
         size_t bytes = 0;
+        std::vector<void*> retired;   // outgrown buffers: kept, a captured graph may name them
     };
     std::mutex ws_mu;
-    std::unordered_map<std::string, Workspace> ws;
-    std::vector<void*> ws_retired;   // outgrown buffers: kept, a captured graph may name them
+    std::unordered_map<std::string, Workspace> ws;   // freed by fa_release_stream_workspace
     // Host-slice calls: one device staging allocation, one pinned ring and
     // one stream per device.
     std::mutex io_mu;
@@ -513,8 +513,7 @@ constexpr size_t kWorkspaceCacheMax = size_t(256) << 20;
 // outgrown buffer is kept, not freed, since work already queued on the stream
 // -- or a graph captured earlier -- may still use it.  hipStreamPerThread
 // names a different stream in every thread, so its key includes the thread.
-int stream_workspace(int dev, hipStream_t stream, size_t bytes, void** out) {
-    DeviceState& s = g_dev[dev];
+std::string workspace_key(hipStream_t stream) {
     char key[64];
     if (stream == hipStreamPerThread) {
         const size_t tid = std::hash<std::thread::id>{}(std::this_thread::get_id());
@@ -522,6 +521,22 @@ int stream_workspace(int dev, hipStream_t stream, size_t bytes, void** out) {
     } else {
         std::snprintf(key, sizeof(key), "%p", reinterpret_cast<void*>(stream));
     }
+    return key;
+}
+
+// Device memory free right now (0 when the query fails).
+size_t free_device_bytes() {
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return free_b;
+}
+
+int stream_workspace(int dev, hipStream_t stream, size_t bytes, void** out) {
+    DeviceState& s = g_dev[dev];
+    const std::string key = workspace_key(stream);
     std::lock_guard<std::mutex> lock(s.ws_mu);
     DeviceState::Workspace& w = s.ws[key];
     if (w.ptr && w.bytes >= bytes) {
@@ -534,7 +549,7 @@ int stream_workspace(int dev, hipStream_t stream, size_t bytes, void** out) {
         (void)hipGetLastError();
         return FA_ERR_ALLOC;
     }
-    if (w.ptr) s.ws_retired.push_back(w.ptr);
+    if (w.ptr) w.retired.push_back(w.ptr);
     w.ptr = ptr;
     w.bytes = want;
     *out = ptr;
@@ -591,9 +606,10 @@ int run_device(int variant, hipStream_t stream, const void* q, const void* k, co
     } else if (cached) {
         rc = stream_workspace(dev, stream, bytes, reinterpret_cast<void**>(&ws));
         if (rc != FA_OK) return rc;
-    } else if (hipMallocAsync(reinterpret_cast<void**>(&ws), bytes, stream) != hipSuccess) {
+    } else if (bytes > free_device_bytes() ||
+               hipMallocAsync(reinterpret_cast<void**>(&ws), bytes, stream) != hipSuccess) {
         (void)hipGetLastError();
-        return FA_ERR_ALLOC;
+        return FA_ERR_ALLOC;   // nothing queued, out untouched
     }
     const int D = pad_d(d);
     const size_t parts = bh * (size_t)plan.p.nqt * plan.p.num_splits;
@@ -813,7 +829,12 @@ int run_naive_device(hipStream_t stream, const float* q, const float* k, const f
 
     const bool f64 = precision == FA_NAIVE_F64;
     const size_t head_bytes = sq * sk * (f64 ? 8 : 4);
-    size_t chunk = head_bytes ? std::max<size_t>(1, kNaiveChunkBytes / head_bytes) : bh;
+    // Score buffer: as many whole heads as fit in kNaiveChunkBytes and half
+    // the free device memory (at least one); a head larger than half the
+    // free memory is refused before anything is queued.
+    const size_t half_free = head_bytes ? free_device_bytes() / 2 : 0;
+    if (head_bytes && head_bytes > half_free) return FA_ERR_ALLOC;
+    size_t chunk = head_bytes ? std::max<size_t>(1, std::min(kNaiveChunkBytes, half_free) / head_bytes) : bh;
     chunk = std::min({chunk, bh, (size_t)65535, imax / sq});
     void* s = nullptr;
     if (head_bytes) {
@@ -1004,6 +1025,31 @@ int fa_device_ex(int variant, void* stream, const float* q, const float* k, cons
     if (opts && opts->dtype != FA_DTYPE_F32) return FA_ERR_INVALID_ARG;   // 16-bit inputs: fa_device_lp
     return run_device(variant, static_cast<hipStream_t>(stream), q, k, v, batch * heads, sq, sk, d,
                       cfg ? cfg->causal : 0, opts, out);
+}
+
+int fa_release_stream_workspace(void* stream) {
+    int dev;
+    int rc = current_device(&dev);
+    if (rc != FA_OK) return rc;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    DeviceState& s = g_dev[dev];
+    std::lock_guard<std::mutex> lock(s.ws_mu);
+    auto it = s.ws.find(workspace_key(st));
+    if (it == s.ws.end()) return FA_OK;
+    // Work queued on the stream may still use the buffers.
+    if (hipStreamSynchronize(st) != hipSuccess) {
+        (void)hipGetLastError();
+        return FA_ERR_COPY;
+    }
+    rc = FA_OK;
+    it->second.retired.push_back(it->second.ptr);
+    for (void* p : it->second.retired)
+        if (p && hipFree(p) != hipSuccess) {
+            (void)hipGetLastError();
+            rc = FA_ERR_ALLOC;
+        }
+    s.ws.erase(it);
+    return rc;
 }
 
 int fa_device_ex_noalloc(int variant, void* stream, const float* q, const float* k, const float* v, size_t batch,

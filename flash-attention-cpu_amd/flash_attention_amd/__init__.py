@@ -64,7 +64,8 @@ EXPORTED_SYMBOLS = (
     "fa_status_string", "fa_config_default",
     "fa_v1", "fa_v2", "fa_v3", "fa_attention",
     "fa_multihead_v1", "fa_multihead_v2", "fa_multihead_v3", "fa_attention_multihead",
-    "fa_device_v1", "fa_device_v2", "fa_device_v3", "fa_device_ex", "fa_device_ex_noalloc",
+    "fa_device_v1", "fa_device_v2", "fa_device_v3", "fa_release_stream_workspace",
+    "fa_device_ex", "fa_device_ex_noalloc",
     "fa_device_lp", "fa_multihead_lp",
     "fa_naive_attention", "fa_naive_device",
     "fa_init", "fa_describe_launch",
@@ -150,6 +151,8 @@ def lib() -> ctypes.CDLL:
     for name in ("fa_device_v1", "fa_device_v2", "fa_device_v3"):
         getattr(L, name).argtypes = dev
         getattr(L, name).restype = ctypes.c_int
+    L.fa_release_stream_workspace.argtypes = [ctypes.c_void_p]
+    L.fa_release_stream_workspace.restype = ctypes.c_int
     L.fa_device_ex.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                ctypes.c_void_p, _SZ, _SZ, _SZ, _SZ, _SZ, _CFG, _OPTS, ctypes.c_void_p]
     L.fa_device_ex.restype = ctypes.c_int
@@ -362,6 +365,11 @@ def attention_device_noalloc(variant: int, q_ptr: int, k_ptr: int, v_ptr: int, b
                                       ctypes.c_void_p(k_ptr), ctypes.c_void_p(v_ptr), batch, heads, seq_len_q,
                                       seq_len_k, d_head, ctypes.byref(cfg), ctypes.byref(opts),
                                       ctypes.c_void_p(out_ptr)))
+
+
+def release_stream_workspace(stream: int = 0) -> None:
+    """Free the split workspace kept for `stream` (fa_release_stream_workspace)."""
+    _check(lib().fa_release_stream_workspace(ctypes.c_void_p(stream)))
 
 
 def describe_launch(variant: int, batch: int, heads: int, seq_len_q: int, seq_len_k: int, d_head: int,

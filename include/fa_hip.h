@@ -42,7 +42,8 @@ extern "C" {
                                  than 256 on the automatic path run the naive kernels) */
 #define FA_ERR_NO_DEVICE 7    /* no HIP device visible */
 #define FA_ERR_MODULE 8       /* code object missing / unloadable (FA_HIP_MODULE) */
-#define FA_ERR_ALLOC 9        /* device allocation failed */
+#define FA_ERR_ALLOC 9        /* device allocation failed, or the request exceeds the free
+                                 device memory (checked before anything is queued) */
 #define FA_ERR_LAUNCH 10      /* kernel launch failed */
 #define FA_ERR_COPY 11        /* host<->device copy or synchronisation failed */
 #define FA_ERR_SCRATCH 12     /* fa_device_ex_noalloc: the call needs more split workspace than
@@ -124,11 +125,12 @@ int fa_attention_multihead(const float* q, size_t q_len, const float* k, size_t 
  * and a key split on grids smaller than the GPU.  Their partials go to a
  * workspace kept per stream (up to 256 MiB; larger ones are allocated and
  * released stream-ordered around the call): the first call on a stream that
- * needs more allocates it with hipMalloc, and buffers are not freed before
- * the process ends, so graphs captured with these calls stay valid.  Calls
- * on one stream share its buffer in stream order; a stream handle value
- * reused after hipStreamDestroy inherits the buffer, so synchronise a stream
- * before destroying it if its handle may be reused for concurrent work.
+ * needs more allocates it with hipMalloc, and buffers are kept (outgrown ones
+ * included) until fa_release_stream_workspace or the end of the process, so
+ * graphs captured with these calls stay valid.  Calls on one stream share
+ * its buffer in stream order; a stream handle value reused after
+ * hipStreamDestroy inherits the buffer, so release a stream's workspace (or
+ * synchronise it) before destroying it if its handle may be reused.
  * These have no single counterpart in the reference (its API takes host
  * slices); they are the device form of the multihead entry points. */
 int fa_device_v1(void* stream, const float* q, const float* k, const float* v, size_t batch,
@@ -140,6 +142,13 @@ int fa_device_v2(void* stream, const float* q, const float* k, const float* v, s
 int fa_device_v3(void* stream, const float* q, const float* k, const float* v, size_t batch,
                  size_t heads, size_t seq_len_q, size_t seq_len_k, size_t d_head,
                  const fa_config* config, float* out);
+/* Frees the split workspace kept for `stream` on the current device (and the
+ * buffers it outgrew), after synchronising the stream.  For servers that
+ * create and destroy streams: call it before hipStreamDestroy.  Graphs
+ * captured with split calls on `stream` must not be replayed afterwards.  A
+ * later split call on the stream allocates a new workspace.  No counterpart
+ * in the reference (the crate's scratch is per call). */
+int fa_release_stream_workspace(void* stream);
 
 /* ---- extension: explicit scale and path control ------------------------
  * Not in the reference.  softmax_scale <= 0 or NaN keeps the reference's

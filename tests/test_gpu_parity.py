@@ -714,3 +714,86 @@ def test_split_workspace_per_stream_and_graph_replay():
         queue(big, torch.cuda.current_stream())
         torch.cuda.synchronize()
         assert_parity(small[1 + rep % 2][3].cpu().numpy(), want[id(small[1 + rep % 2])], f"eager after replay {rep}")
+
+
+def test_release_stream_workspace_returns_device_memory():
+    """A split call keeps its partials in a workspace per stream; releasing it
+    gives the memory back.  Forced split-KV with 128 key splits over 64 heads
+    of 64 queries at d64: about 138 MB of partials per stream.  Each of six
+    streams gets a call, its output (bit-identical to the same call on the
+    default stream), a check that the device lost at least the workspace,
+    the release, and a check that the memory came back."""
+    torch = _torch()
+    dev = torch.device("cuda", 0)
+    bh, sq, sk, d, splits = 64, 64, 8192, 64, 128
+    s = fa.describe_launch(2, 1, bh, sq, sk, d, False, fa.PATH_SPLITKV, splits)
+    ws = int(s.split("workspace=")[1])
+    assert 100e6 < ws < 256 << 20, s
+    rng = np.random.default_rng(77)
+    t = [torch.from_numpy(rng.standard_normal(n, dtype=np.float32)).to(dev) for n in (bh * sq * d, bh * sk * d,
+                                                                                      bh * sk * d)]
+    out = torch.zeros(bh * sq * d, device=dev)
+
+    def call(stream):
+        fa.attention_device(2, t[0].data_ptr(), t[1].data_ptr(), t[2].data_ptr(), 1, bh, sq, sk, d, False,
+                            out.data_ptr(), stream, path=fa.PATH_SPLITKV, num_splits=splits)
+
+    call(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    want = out.cpu().numpy().copy()
+    for i in range(6):
+        st = torch.cuda.Stream()
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]
+        out.zero_()
+        torch.cuda.synchronize()
+        call(st.cuda_stream)
+        st.synchronize()
+        assert np.array_equal(out.cpu().numpy(), want), i
+        free1 = torch.cuda.mem_get_info()[0]
+        fa.release_stream_workspace(st.cuda_stream)
+        free2 = torch.cuda.mem_get_info()[0]
+        print(f"[workspace] stream {i}: free before {free0 / 2**20:.0f} MiB, with workspace "
+              f"{free1 / 2**20:.0f} MiB, after release {free2 / 2**20:.0f} MiB", flush=True)
+        assert free0 - free1 >= ws, (free0, free1, ws)
+        assert abs(free2 - free0) < 16 << 20, (free0, free2)
+    fa.release_stream_workspace(torch.cuda.current_stream().cuda_stream)
+    fa.release_stream_workspace(torch.cuda.current_stream().cuda_stream)   # nothing kept: still FA_OK
+
+
+def test_requests_beyond_device_memory_fail_cleanly():
+    """FA_ERR_ALLOC before anything is queued, out untouched, the library
+    usable afterwards: (a) the naive path of a d_head > 256 head whose score
+    matrix (2^19 x 2^19 f32 = 1 TiB) exceeds the device; (b) a forced split
+    of 32 heads x 16384 queries x 1024 key splits at d256 (551 GB of
+    partials)."""
+    torch = _torch()
+    dev = torch.device("cuda", 0)
+    n, d = 1 << 19, 300
+    q = torch.zeros(n * d, device=dev)
+    out = torch.full((n * d,), 5.0, device=dev)
+    with pytest.raises(fa.FaError) as e:
+        fa.attention_device(2, q.data_ptr(), q.data_ptr(), q.data_ptr(), 1, 1, n, n, d, False, out.data_ptr(),
+                            torch.cuda.current_stream().cuda_stream)
+    assert e.value.status == fa.FA_ERR_ALLOC
+    torch.cuda.synchronize()
+    assert bool((out == 5.0).all())
+    del q, out
+    bh, sq, sk, d = 32, 16384, 65536, 256
+    s = fa.describe_launch(2, 1, bh, sq, sk, d, False, fa.PATH_SPLITKV, 1024)
+    assert int(s.split("workspace=")[1]) > 400e9, s
+    q = torch.zeros(bh * sq * d, device=dev)
+    kv = torch.zeros(bh * sk * d, device=dev)
+    out = torch.full((bh * sq * d,), 5.0, device=dev)
+    with pytest.raises(fa.FaError) as e:
+        fa.attention_device(2, q.data_ptr(), kv.data_ptr(), kv.data_ptr(), 1, bh, sq, sk, d, False, out.data_ptr(),
+                            torch.cuda.current_stream().cuda_stream, path=fa.PATH_SPLITKV, num_splits=1024)
+    assert e.value.status == fa.FA_ERR_ALLOC
+    torch.cuda.synchronize()
+    assert bool((out == 5.0).all())
+    del q, kv, out
+    torch.cuda.empty_cache()
+    q = random_vec(64 * 32, 5)
+    want = cpu_v2(q, q, q, 1, 64, 64, 32, True)
+    got = _device_run(2, q, q, q, 1, 64, 64, 32, True)
+    assert_parity(got, want, "after FA_ERR_ALLOC")
