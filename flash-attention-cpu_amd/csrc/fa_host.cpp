@@ -534,11 +534,37 @@ size_t free_device_bytes() {
     return free_b;
 }
 
+//
+// A call captured into a graph takes the buffer over: it moves to the
+// stream's retired list (kept until fa_release_stream_workspace), and the
+// next eager call on the stream gets a new one.  So replays of the graph --
+// on any stream -- never share partials with later eager calls on the
+// capture stream, nor with another graph captured there.
 int stream_workspace(int dev, hipStream_t stream, size_t bytes, void** out) {
     DeviceState& s = g_dev[dev];
     const std::string key = workspace_key(stream);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess) {
+        (void)hipGetLastError();
+        cap = hipStreamCaptureStatusNone;
+    }
+    const bool capturing = cap == hipStreamCaptureStatusActive;
     std::lock_guard<std::mutex> lock(s.ws_mu);
     DeviceState::Workspace& w = s.ws[key];
+    if (capturing) {
+        void* ptr = nullptr;
+        if (w.ptr && w.bytes >= bytes) {
+            ptr = w.ptr;
+            w.ptr = nullptr;
+            w.bytes = 0;
+        } else if (hipMalloc(&ptr, bytes) != hipSuccess) {
+            (void)hipGetLastError();
+            return FA_ERR_ALLOC;
+        }
+        w.retired.push_back(ptr);
+        *out = ptr;
+        return FA_OK;
+    }
     if (w.ptr && w.bytes >= bytes) {
         *out = w.ptr;
         return FA_OK;

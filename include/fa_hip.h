@@ -127,7 +127,10 @@ int fa_attention_multihead(const float* q, size_t q_len, const float* k, size_t 
  * released stream-ordered around the call): the first call on a stream that
  * needs more allocates it with hipMalloc, and buffers are kept (outgrown ones
  * included) until fa_release_stream_workspace or the end of the process, so
- * graphs captured with these calls stay valid.  Calls on one stream share
+ * graphs captured with these calls stay valid.  A call made under graph
+ * capture takes the stream's buffer over for the graph (make one eager call
+ * on the stream before each capture; the next eager call allocates anew), so
+ * replays never share partials with other calls.  Calls on one stream share
  * its buffer in stream order; a stream handle value reused after
  * hipStreamDestroy inherits the buffer, so release a stream's workspace (or
  * synchronise it) before destroying it if its handle may be reused.

@@ -797,3 +797,53 @@ def test_requests_beyond_device_memory_fail_cleanly():
     want = cpu_v2(q, q, q, 1, 64, 64, 32, True)
     got = _device_run(2, q, q, q, 1, 64, 64, 32, True)
     assert_parity(got, want, "after FA_ERR_ALLOC")
+
+
+def test_captured_calls_own_their_workspace():
+    """A split call captured into a graph takes its stream's workspace over,
+    so replays never share partials with later eager calls on the capture
+    stream.  Two graphs are captured on one stream (an eager call before each
+    capture makes the buffer the capture takes), then replayed on two other
+    streams while an eager split call of a third shape runs on the capture
+    stream, with no synchronisation between them; every output must match
+    its reference, on every repetition."""
+    torch = _torch()
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(94)
+
+    def make(bh, sq, sk, d):
+        arrs = [rng.standard_normal(n, dtype=np.float32) for n in (bh * sq * d, bh * sk * d, bh * sk * d)]
+        t = [torch.from_numpy(a).to(dev) for a in arrs]
+        return (bh, sq, sk, d), arrs, t, torch.zeros(bh * sq * d, device=dev)
+
+    cases = [make(4, 1, 3000, 128), make(2, 16, 2000, 64), make(3, 3, 1500, 128)]
+    want = [cpu_v2(*c[1], *c[0], False) for c in cases]
+
+    def queue(case, stream):
+        (bh, sq, sk, d), _, (tq, tk, tv), out = case
+        fa.attention_device(2, tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), 1, bh, sq, sk, d, False,
+                            out.data_ptr(), stream.cuda_stream)
+
+    gs, r1, r2 = torch.cuda.Stream(), torch.cuda.Stream(), torch.cuda.Stream()
+    graphs = []
+    for case in cases[:2]:
+        queue(case, gs)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=gs):
+            queue(case, gs)
+        graphs.append(g)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        for c in cases:
+            c[3].fill_(7.0)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(r1):
+            graphs[0].replay()
+        with torch.cuda.stream(r2):
+            graphs[1].replay()
+        queue(cases[2], gs)
+        torch.cuda.synchronize()
+        for i, c in enumerate(cases):
+            assert_parity(c[3].cpu().numpy(), want[i], f"rep {rep} case {i}")
+    fa.release_stream_workspace(gs.cuda_stream)
