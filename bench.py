@@ -10,8 +10,9 @@ the launch stream) against the FP32-MFMA peak, and ``roofline.traffic`` is
 the kernel's measured HBM bytes per launch (rocprofv3 counters, reported only
 while the kernel sources match the ones profiled).
 
-Every other configuration (1, 3, 4a, 4b, 5, 5c; v1/v2/v3) is timed the same
-way into ``extra.configs`` -- TFLOP/s and % of the FP32-MFMA peak for
+Every other configuration (1, 3, 4a, 4b, 5, 5c; v1/v2/v3), and two wide-head
+shapes beyond BASELINE.json (d_head 512 and 1024), is timed the same way into
+``extra.configs`` -- TFLOP/s and % of the FP32-MFMA peak for
 prefill shapes, GB/s and % of 8 TB/s for decode shapes -- next to a CPU
 baseline on the same inputs: the oracle's v2 (oracle/, a C restatement of the
 reference crate's rayon + AVX-512/AVX2 path, src/v2.rs:160-385) on all host
@@ -52,6 +53,10 @@ CONFIGS = [
     ("config4b", 32, 16, 32768, 128, False, 1.0, False, "decode"),
     ("config5", 16, 4096, 1024, 256, False, 3.0, True, "prefill"),
     ("config5c", 16, 1000, 1000, 256, True, 3.0, True, "prefill"),
+    # not BASELINE.json configs: heads wider than 256 on the column-group
+    # flash kernels (the crate's flash path takes any d_head)
+    ("wide_d512", 16, 2048, 2048, 512, True, 1.0, False, "prefill"),
+    ("wide_d1024", 8, 2048, 2048, 1024, True, 1.0, False, "prefill"),
 ]
 HEADLINE = "config2"
 

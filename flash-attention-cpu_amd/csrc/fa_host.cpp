@@ -37,7 +37,8 @@
 namespace {
 
 constexpr int kMaxDevices = 64;
-constexpr int kMaxD = 256;
+constexpr int kMaxD = 1024;         // widest head of the f32 flash kernels
+constexpr int kMaxDNarrow = 256;    // 16-bit kernels and the split-KV decoders
 constexpr int kDecodeRows = 16;     // query rows per split-KV wave
 constexpr int kDecodeWaves = 4;     // waves per split-KV workgroup
 constexpr int kRowsMaxQ = 4;        // row-streaming decode: most query rows
@@ -259,7 +260,9 @@ int pad_d(size_t d) {
     if (d <= 32) return 32;
     if (d <= 64) return 64;
     if (d <= 128) return 128;
-    return 256;
+    if (d <= 256) return 256;
+    if (d <= 512) return 512;
+    return 1024;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -277,6 +280,9 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     if ((path == FA_PATH_SPLITKV || path == FA_PATH_SPLITKV_ROWS) && variant == 1) return FA_ERR_INVALID_ARG;
     if (opts && opts->num_splits < 0) return FA_ERR_INVALID_ARG;
     if (d > (size_t)kMaxD) return FA_ERR_UNSUPPORTED;
+    // d_head > 256: f32 prefill kernels only (column groups; key split allowed)
+    const bool wide = d > (size_t)kMaxDNarrow;
+    if (wide && (lp || path == FA_PATH_SPLITKV || path == FA_PATH_SPLITKV_ROWS)) return FA_ERR_UNSUPPORTED;
     const size_t imax = 0x7fffffff;
     if (sq > imax || sk > imax || bh > imax) return FA_ERR_UNSUPPORTED;
 
@@ -303,7 +309,7 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     const size_t nqt = (sq + kDecodeRows - 1) / kDecodeRows;
     // Row-streaming decode: 16-byte loads; f32 with seq_q <= 4, or 16-bit
     // with seq_q = 1 and D >= 64.
-    const bool rows_ok = vec && (lp ? (sq == 1 && D >= 64) : sq <= (size_t)kRowsMaxQ);
+    const bool rows_ok = !wide && vec && (lp ? (sq == 1 && D >= 64) : sq <= (size_t)kRowsMaxQ);
     if (path == FA_PATH_SPLITKV_ROWS && !rows_ok) return FA_ERR_UNSUPPORTED;
     bool split = false;
     if (variant != 1) {
@@ -321,7 +327,7 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
             // they take split-KV only where the row kernel applies.
             const bool decode_shape = sq <= 64 && sk >= 512;
             const bool few_tiles = !lp && nqt * bh * 2 <= (size_t)num_cus && sk >= 256;
-            split = (decode_shape || few_tiles) && (!lp || rows_ok);
+            split = !wide && (decode_shape || few_tiles) && (!lp || rows_ok);
         }
     }
     const bool row_decode = split && rows_ok && (path == FA_PATH_SPLITKV_ROWS || path == FA_PATH_AUTO);
@@ -344,8 +350,9 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
             std::snprintf(buf, sizeof(buf), "fa_prefill_lp_%s_d%d_%d_t%d", dtype == FA_DTYPE_BF16 ? "bf16" : "f16",
                           D, vec ? 2 : 0, lp_tiles);
         } else {
-            // 0: scalar loads (any d), 1: 128-bit loads, 2: global->LDS DMA (v3)
-            const int loader = vec ? (variant == 3 ? 2 : 1) : 0;
+            // 0: scalar loads (any d), 1: 128-bit loads, 2: global->LDS DMA (v3
+            // with two LDS stages; D = 1024 holds one)
+            const int loader = vec ? (fa_prefill_nbuf(D, variant) == 2 ? 2 : 1) : 0;
             std::snprintf(buf, sizeof(buf), "fa_prefill_v%d_d%d_%d", variant, D, loader);
         }
         plan->first.name = buf;
@@ -585,10 +592,11 @@ int stream_workspace(int dev, hipStream_t stream, size_t bytes, void** out) {
 int run_naive_device(hipStream_t stream, const float* q, const float* k, const float* v, size_t bh, size_t sq,
                      size_t sk, size_t d, int causal, int precision, float* out, float scale);
 
-// Heads wider than the flash kernels' 256 columns (the crate takes any
+// Heads wider than the flash kernels' 1024 columns (the crate takes any
 // d_head): f32 inputs on the automatic path run the naive kernels over a
 // materialised score matrix (src/naive.rs:14-75, in f32 with the same
-// 1/sqrt(d) or explicit scale).  FA_OK when that applies, else the status.
+// 1/sqrt(d) or explicit scale), in head chunks capped by free device
+// memory.  FA_OK when that applies, else the status.
 int wide_head_status(int variant, const fa_launch_opts* opts) {
     if (variant < 1 || variant > 3) return FA_ERR_INVALID_ARG;
     if (opts && (opts->dtype != FA_DTYPE_F32 || opts->path != FA_PATH_AUTO || opts->num_splits > 0))
@@ -943,7 +951,7 @@ const char* fa_status_string(int status) {
         case FA_ERR_V_SHAPE: return "v shape mismatch";
         case FA_ERR_OUT_SHAPE: return "out shape mismatch";
         case FA_ERR_INVALID_ARG: return "invalid argument";
-        case FA_ERR_UNSUPPORTED: return "unsupported shape (d_head > 256 off the automatic f32 path, or size beyond 32-bit indexing)";
+        case FA_ERR_UNSUPPORTED: return "unsupported shape (d_head > 256 with 16-bit inputs or split-KV, d_head > 1024 off the automatic f32 path, or size beyond 32-bit indexing)";
         case FA_ERR_NO_DEVICE: return "no HIP device available";
         case FA_ERR_MODULE: return "cannot load the gfx950 code object (fa_kernels.hsaco / FA_HIP_MODULE)";
         case FA_ERR_ALLOC: return "device allocation failed";
@@ -1107,7 +1115,7 @@ int fa_multihead_lp(int dtype, const void* q, size_t q_len, const void* k, size_
     if (out_len != bh * sq * d) return FA_ERR_OUT_SHAPE;
     if (bh == 0 || sq == 0 || sk == 0 || d == 0) return FA_OK;   // out untouched
     if (!q || !k || !v || !out) return FA_ERR_INVALID_ARG;
-    if (d > (size_t)kMaxD) return FA_ERR_UNSUPPORTED;   // before any copy: the 16-bit kernels stop at 256
+    if (d > (size_t)kMaxDNarrow) return FA_ERR_UNSUPPORTED;   // before any copy: the 16-bit kernels stop at 256
     const int causal = cfg ? cfg->causal : 0;
     const fa_launch_opts o{0.0f, FA_PATH_AUTO, 0, dtype};
     return with_host_slices(q, k, v, 2, bh, sq, sk, d, out,
@@ -1139,7 +1147,7 @@ int fa_describe_launch(int variant, size_t batch, size_t heads, size_t sq, size_
         if (d > (size_t)kMaxD) {
             rc = wide_head_status(variant, opts);
             if (rc == FA_OK)
-                text = "fa_naive_scores_f32; fa_naive_softmax_f32; fa_naive_pv_f32 (d_head > 256: materialised scores)";
+                text = "fa_naive_scores_f32; fa_naive_softmax_f32; fa_naive_pv_f32 (d_head > 1024: materialised scores)";
         } else {
             rc = make_plan(variant, dummy, dummy, dummy, dummy, bh, sq, sk, d, causal, opts, num_cus, &plan);
         }

@@ -15,9 +15,10 @@
 // All arithmetic is IEEE f32 (f32 MFMA, no reduced-precision inputs); the
 // naive kernels also have an f64 instantiation for on-device checking.
 //
-// Prefill geometry (D = d_head padded to 32/64/128/256; fa_params.h):
+// Prefill geometry (D = d_head padded to 32/64/128/256/512/1024; fa_params.h):
 //   * a workgroup of NW = 8 waves owns BQ = 128 query rows of one
-//     (batch*head) slice; wave w owns rows 16w .. 16w+15;
+//     (batch*head) slice; wave w owns rows 16w .. 16w+15 (D > 256: column
+//     groups of D/256 waves share a 16-row tile, 256 columns each);
 //   * keys stream through LDS in stages of SK keys (64 for D <= 128, 32 or
 //     16 for D = 256), K rows padded to D+8 floats and V rows to D+16 (D+8
 //     at D = 32) so 128-bit reads are free of bank conflicts on the 128-bank
@@ -283,21 +284,28 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     constexpr int BQ = fa_prefill_rows(D);    // query rows per workgroup
     constexpr int SK = fa_prefill_stage_keys(D, VARIANT);   // keys per LDS stage
     constexpr int KB = SK / 16;               // 16-key blocks per stage
-    constexpr int NQ = D / 4;                 // MFMA k-steps over d
-    constexpr int NC = D / 16;                // 128-bit K reads per lane per key block
-    constexpr int VW = (D >= 64) ? 4 : 2;     // floats per lane per V read
-    constexpr int NVR = (D >= 64) ? D / 64 : 1;   // V reads per key
-    constexpr int NOB = D / 16;               // O^T accumulator blocks
+    // Column groups (D > 256): CG waves share a 16-row tile, each holding DW
+    // columns of Q and O; their partial scores are summed through LDS.
+    constexpr int CG = fa_prefill_cgroups(D);
+    constexpr int DW = D / CG;                // columns per wave
+    constexpr int TILES = NW / CG;            // 16-row tiles per workgroup
+    constexpr int NQ = DW / 4;                // MFMA k-steps over the wave's columns
+    constexpr int NC = DW / 16;               // 128-bit K reads per lane per key block
+    constexpr int VW = (DW >= 64) ? 4 : 2;    // floats per lane per V read
+    constexpr int NVR = (DW >= 64) ? DW / 64 : 1;   // V reads per key
+    constexpr int NOB = DW / 16;              // O^T accumulator blocks
     constexpr int CPR = D / 4;                // 16-byte chunks per row
     constexpr int LDK = kpad_row<D>();        // padded K row (floats)
     constexpr int LDV = vpad_row<D>();        // padded V row (floats)
     constexpr int KTILE = SK * LDK;           // floats per K stage
     constexpr int VTILE = SK * LDV;           // floats per V stage
     constexpr bool DMA = (LOADER == 2);
-    constexpr int NBUF = (VARIANT == 3) ? 2 : 1;
+    constexpr int NBUF = fa_prefill_nbuf(D, VARIANT);
+    constexpr bool PIPE = NBUF == 2;          // v3's double-buffered schedule
     static_assert(NVR * VW == NOB, "V read layout");
-    static_assert(!DMA || VARIANT == 3, "LDS DMA needs the double-buffered pipeline");
+    static_assert(!DMA || PIPE, "LDS DMA needs the double-buffered pipeline");
     static_assert((SK * CPR) % NT == 0, "stage load must split evenly");
+    static_assert(BQ == 16 * TILES && CG * DW == D, "column groups");
 
     // Separate arrays so the compiler can tell a DMA in flight into one
     // buffer from LDS reads of another (no needless vmcnt waits).
@@ -305,10 +313,17 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     __shared__ __attribute__((aligned(16))) float Vb0[VTILE];
     __shared__ __attribute__((aligned(16))) float Kb1[NBUF > 1 ? KTILE : 4];
     __shared__ __attribute__((aligned(16))) float Vb1[NBUF > 1 ? VTILE : 4];
+    // Column groups: per-wave partial scores, one slot per wave (two in the
+    // pipelined schedule, which has one barrier per stage).
+    constexpr int XSLOTS = CG > 1 ? (PIPE ? 2 : 1) : 0;
+    __shared__ __attribute__((aligned(16))) f32x4 Xs[XSLOTS ? XSLOTS * NW * KB * 64 : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tile = CG > 1 ? wave % TILES : wave;   // the wave's 16-row tile
+    const int cgrp = CG > 1 ? wave / TILES : 0;      // its column group
+    const int c0 = cgrp * DW;                 // its first column of Q and O
     const int g = lane >> 4;                  // lane group 0..3
     const int li = lane & 15;
 
@@ -330,17 +345,17 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     const float c = p.scale_log2e;
     const bool causal = p.causal != 0;
 
-    // Q rows of this wave as the B operand: lane holds Q[row][16cc + 4g + i],
-    // pre-multiplied by scale * log2(e) so scores come out of the MFMA in the
-    // exp2 domain (src/v2.rs:171-173 multiplies after the dot; the product
-    // differs by one f32 rounding per element of Q).
-    int row_first = q0 + 16 * wave;
+    // Q rows of this wave as the B operand: lane holds Q[row][c0 + 16cc + 4g
+    // + i], pre-multiplied by scale * log2(e) so scores come out of the MFMA
+    // in the exp2 domain (src/v2.rs:171-173 multiplies after the dot; the
+    // product differs by one f32 rounding per element of Q).
+    int row_first = q0 + 16 * tile;
     int qrow = row_first + li;
     float qreg[NQ];
     auto load_q = [&](int row) {   // unscaled
 #pragma unroll
         for (int cc = 0; cc < NC; ++cc) {
-            const f32x4 t = load4<LOADER != 0>(Qh, row, seq_q, 16 * cc + 4 * g, d);
+            const f32x4 t = load4<LOADER != 0>(Qh, row, seq_q, c0 + 16 * cc + 4 * g, d);
 #pragma unroll
             for (int i = 0; i < 4; ++i) qreg[4 * cc + i] = t[i];
         }
@@ -491,12 +506,14 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     // a ring of PRE + 1 register sets, each read issued after the MFMAs that
     // last used its slot.  D = 256: v2 runs one ahead (230 VGPRs; config 5's
     // shape 577 -> 572.5 us); v1 gains nothing and v3, with its second K / V
-    // buffer, would spill, so they read each operand just before its MFMA.
-    constexpr int PRE = (D <= 128) ? 2 : (VARIANT == 2 ? 1 : 0);
+    // buffer, would spill, so they read each operand just before its MFMA
+    // (as does v2 at D = 1024, where the scalar loader would spill).
+    constexpr int PRE = (DW <= 128) ? 2 : (VARIANT == 2 && D <= 512 ? 1 : 0);
     f32x4 kpre[PRE ? PRE : 1][KB];
     auto k_chunk = [&](const float* Ks, int cc, f32x4* dst) {
 #pragma unroll
-        for (int b = 0; b < KB; ++b) dst[b] = *reinterpret_cast<const f32x4*>(Ks + lds_off<LDK>(16 * b + li, 4 * cc + g));
+        for (int b = 0; b < KB; ++b)
+            dst[b] = *reinterpret_cast<const f32x4*>(Ks + lds_off<LDK>(16 * b + li, c0 / 4 + 4 * cc + g));
     };
     auto qk_preload = [&](const float* Ks) {
         if constexpr (PRE > 0) {
@@ -565,13 +582,36 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         }
     };
 
+    // Column groups: each wave's QK^T covers its DW columns (group 0's chain
+    // starts from -m); xs_put stores that partial in the wave's slot and,
+    // after a barrier, xs_sum adds the tile's CG partials in group order, so
+    // every wave of the tile holds bit-identical scores and runs the same
+    // softmax (m, l and the lazy-max decisions agree across the group).
+    auto xs_put = [&](const f32x4* s, int slot) {
+        if constexpr (CG > 1) {
+#pragma unroll
+            for (int b = 0; b < KB; ++b) Xs[((slot * NW + wave) * KB + b) * 64 + lane] = s[b];
+        }
+    };
+    auto xs_sum = [&](f32x4* s, int slot) {
+        if constexpr (CG > 1) {
+#pragma unroll
+            for (int b = 0; b < KB; ++b) {
+                f32x4 t = Xs[((slot * NW + tile) * KB + b) * 64 + lane];
+#pragma unroll
+                for (int j = 1; j < CG; ++j) t += Xs[((slot * NW + j * TILES + tile) * KB + b) * 64 + lane];
+                s[b] = t;
+            }
+        }
+    };
+
     // V operands of PV step `step` (keys 16(step/4) + 4g + step%4).
     auto read_v = [&](const float* Vs, int step, f32x4* vv) {
         const int kr = 16 * (step / 4) + 4 * g + (step % 4);
 #pragma unroll
         for (int hh = 0; hh < NVR; ++hh) {
             if constexpr (VW == 4) {
-                vv[hh] = *reinterpret_cast<const f32x4*>(Vs + lds_off<LDV>(kr, 16 * hh + li));
+                vv[hh] = *reinterpret_cast<const f32x4*>(Vs + lds_off<LDV>(kr, c0 / 4 + 16 * hh + li));
             } else {
                 const f32x2 t = *reinterpret_cast<const f32x2*>(Vs + lds_off<LDV>(kr, li >> 1) + 2 * (li & 1));
                 vv[hh] = (f32x4){t[0], t[1], 0.0f, 0.0f};
@@ -617,7 +657,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
 #pragma unroll
             for (int b = 0; b < KB; ++b) s[b] -= delta;
             if (grow) m = (seen ? m : 0.0f) + delta;
-            const float nm = (m == FA_NEG_INF) ? 0.0f : -m;
+            const float nm = (m == FA_NEG_INF || cgrp != 0) ? 0.0f : -m;   // -m only in group 0's chain
             nref = (f32x4){nm, nm, nm, nm};
         }
 #pragma unroll
@@ -716,7 +756,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             for (int hh = 0; hh < NVR; ++hh)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int dv0 = 64 * hh + VW * (4 * g + r);
+                    const int dv0 = c0 + 64 * hh + VW * (4 * g + r);
                     if (LOADER != 0 && dv0 + VW <= d) {
                         if constexpr (VW == 4) {
                             const f32x4 t = {o[4 * hh][r] * inv, o[4 * hh + 1][r] * inv, o[4 * hh + 2][r] * inv,
@@ -735,7 +775,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         }
     };
 
-    if constexpr (VARIANT == 3) {
+    if constexpr (PIPE) {
         // Double-buffered K and V (src/v3.rs:445-483: the next tile's scores
         // are issued before the current tile is finished).  At step st, K(st+2)
         // and V(st+1) stream by DMA into the buffers freed by the previous
@@ -756,7 +796,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         auto kb_of = [&](int gs) { return gs < nA ? k0 + gs * SK : (gs - nA) * SK; };
         auto gstage_active = [&](int gs) -> bool {
             const int kbase = kb_of(gs);
-            const int rf = (gs < nA ? qb * BQ : q0_b) + 16 * wave;
+            const int rf = (gs < nA ? qb * BQ : q0_b) + 16 * tile;
             return kbase < seq_k && !(causal && kbase > rf + 15);
         };
         // Q and K(0) first; V(0) and K(1) stream in under stage 0's QK^T.
@@ -775,14 +815,15 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         // Measured: d = 256 558.6 -> 548.9 us (config 5 shape), d = 64
         // 144.3 -> 143.2 us.  Not at D = 128, where the two loop copies
         // together need more than 256 VGPRs (39 spilled; 274 -> 288 us).
-        constexpr bool EARLY_OK = D != 128;
+        constexpr bool EARLY_OK = D != 128 && CG == 1;
         const bool early = EARLY_OK && FW < NW && fwave < 0;
         f32x4 s_cur[KB];
         bool act_cur = ntot > 0 && gstage_active(0);
         if (act_cur) {
             qk_preload(Kb0);
             qk_stage(Kb0, s_cur);
-            mask_stage(s_cur, kb_of(0));
+            if constexpr (CG > 1) xs_put(s_cur, 0);   // summed and masked after the barrier
+            else mask_stage(s_cur, kb_of(0));
             if (early) softmax_part(s_cur);
         }
         wait_vmcnt<0>();
@@ -798,7 +839,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             if (gs + 2 < ntot) fill_stage(KL, Kh, kb_of(gs + 2), k_fill);
             if (has_next) fill_stage(VL, Vh, kb_of(gs + 1), v_fill);
             const bool switch_now = pairs && gs == nA - 1 && nB > 0;
-            if (switch_now) load_q(q0_b + 16 * wave + li);
+            if (switch_now) load_q(q0_b + 16 * tile + li);
             const bool act_nxt = has_next && gstage_active(gs + 1);
             auto do_switch = [&]() {
                 // block A's rows, full 128-bit stores (two_blocks needs d = D)
@@ -821,7 +862,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
                         }
                 }
                 q0 = q0_b;
-                row_first = q0 + 16 * wave;
+                row_first = q0 + 16 * tile;
                 qrow = row_first + li;
 #pragma unroll
                 for (int j = 0; j < NOB; ++j) o[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
@@ -855,7 +896,14 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
                 // This stage's softmax + PV, then the next stage's QK^T from
                 // the other buffer, with no barrier between them.  Both stages
                 // are resident: their first operands are read before the
-                // softmax.
+                // softmax.  Column groups first sum the tile's partial scores
+                // (slot P, written before the barrier that ended the last step).
+                if constexpr (CG > 1) {
+                    if (act_cur) {
+                        xs_sum(s_cur, P);
+                        mask_stage(s_cur, kb_of(gs));
+                    }
+                }
                 if (act_cur) pv_preload(v_cur);
                 if (act_nxt) qk_preload(k_next);
                 if (act_cur) {
@@ -865,7 +913,8 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
                 if (switch_now) do_switch();
                 if (act_nxt) {
                     qk_stage(k_next, s_cur);
-                    mask_stage(s_cur, kb_of(gs + 1));
+                    if constexpr (CG > 1) xs_put(s_cur, 1 - P);
+                    else mask_stage(s_cur, kb_of(gs + 1));
                 }
             }
             if (has_next) {
@@ -886,25 +935,37 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         else run_steps(std::false_type{});
     } else {
         // Single LDS stage; the next stage's global loads are issued into
-        // registers before the current stage computes.
+        // registers before the current stage computes (D = 1024: its 64
+        // registers would spill, so each stage is loaded when it is stored).
+        constexpr bool PF = LOAD_ITERS <= 4;
         f32x4 kr[LOAD_ITERS], vr[LOAD_ITERS];
-        if (nst > 0) {
+        if (PF && nst > 0) {
             load_regs(Kh, k0, kr);
             load_regs(Vh, k0, vr);
         }
         for (int st = 0; st < nst; ++st) {
+            if (!PF) {
+                load_regs(Kh, k0 + st * SK, kr);
+                load_regs(Vh, k0 + st * SK, vr);
+            }
             store_regs(KL, Kb0, kr);
             store_regs(VL, Vb0, vr);
             __syncthreads();
-            if (st + 1 < nst) {
+            if (PF && st + 1 < nst) {
                 load_regs(Kh, k0 + (st + 1) * SK, kr);
                 load_regs(Vh, k0 + (st + 1) * SK, vr);
             }
-            if (stage_active(st)) {
-                f32x4 s[KB];
+            const bool act = stage_active(st);
+            f32x4 s[KB];
+            if (act) {
                 qk_preload(Kb0);
                 pv_preload(Vb0);
                 qk_stage(Kb0, s);
+                if constexpr (CG > 1) xs_put(s, 0);
+            }
+            if constexpr (CG > 1) __syncthreads();   // the tile's partial scores are in LDS
+            if (act) {
+                xs_sum(s, 0);
                 mask_stage(s, k0 + st * SK);
                 softmax_part(s);
                 pv_part(s, Vb0, no_hook);
@@ -916,13 +977,13 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     if (splitk) {
         // Partial for this wave's 16-row tile and this key split, in the
         // split-KV layout fa_merge reads: O rows (unnormalised), m, l.
-        const int qt = q0 / 16 + wave;
+        const int qt = q0 / 16 + tile;
         if (qt >= p.nqt) return;
         const float lt = row4_sum(l);
         const size_t pidx = ((size_t)bh * p.nqt + qt) * p.num_splits + ysplit;
         float* po = p.part_o + pidx * 16 * D;
         float* pml = p.part_ml + pidx * 32;
-        if (g == 0) {
+        if (g == 0 && cgrp == 0) {   // (m, l) agree across the column group
             pml[li] = m;
             pml[16 + li] = lt;
         }
@@ -930,7 +991,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         for (int hh = 0; hh < NVR; ++hh)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int dv0 = 64 * hh + VW * (4 * g + r);
+                const int dv0 = c0 + 64 * hh + VW * (4 * g + r);
 #pragma unroll
                 for (int j = 0; j < VW; ++j) po[li * D + dv0 + j] = o[VW * hh + j][r];
             }
@@ -1232,6 +1293,30 @@ __device__ __forceinline__ void merge_body(const FaParams& p) {
     for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off);
     __syncthreads();
 
+    if constexpr (CH > 64) {
+        // D > 256: each lane takes chunks lane, lane + 64, ...
+        constexpr int CPL = CH / 64;
+        const float* po = p.part_o + (pbase * 16 + qi) * D + 4 * lane;
+        f32x4 acc[CPL];
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) acc[cc] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int sp = 0; sp < ns; ++sp) {
+            const float w = wts[sp];
+#pragma unroll
+            for (int cc = 0; cc < CPL; ++cc)
+                acc[cc] += *reinterpret_cast<const f32x4*>(po + (size_t)sp * 16 * D + 256 * cc) * w;
+        }
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        float* orow = p.out + (size_t)row * p.d;
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int col = 4 * (lane + 64 * cc) + e;
+                if (col < p.d) orow[col] = acc[cc][e] * inv;
+            }
+        return;
+    }
     const int ch = lane % CH, grp = lane / CH;
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     if (grp < GROUPS) {
@@ -1446,6 +1531,14 @@ FA_PREFILL_ALL(32)
 FA_PREFILL_ALL(64)
 FA_PREFILL_ALL(128)
 FA_PREFILL_ALL(256)
+FA_PREFILL_ALL(512)
+// D = 1024: single-stage v3 (no LDS room for a second stage), so no DMA loader
+FA_PREFILL(1024, 1, 0)
+FA_PREFILL(1024, 1, 1)
+FA_PREFILL(1024, 2, 0)
+FA_PREFILL(1024, 2, 1)
+FA_PREFILL(1024, 3, 0)
+FA_PREFILL(1024, 3, 1)
 
 // Decode register double-buffering (FA_DECODE_DBUF=1) trades occupancy for
 // one block of loads in flight per register set.
@@ -1511,6 +1604,8 @@ FA_MERGE(32)
 FA_MERGE(64)
 FA_MERGE(128)
 FA_MERGE(256)
+FA_MERGE(512)
+FA_MERGE(1024)
 
 #define FA_NAIVE(T, SUF)                                                                          \
     extern "C" __global__ void __launch_bounds__(256) fa_naive_scores_##SUF(NaiveParams p) {       \

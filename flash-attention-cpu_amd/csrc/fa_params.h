@@ -59,17 +59,23 @@ typedef struct NaiveParams {
 #endif
 #ifdef __cplusplus
 constexpr int fa_prefill_waves(int D) { return D <= 128 ? FA_PREFILL_WAVES : 8; }
-constexpr int fa_prefill_rows(int D) { return 16 * fa_prefill_waves(D); }
+// d_head > 256 (D = 512, 1024): column groups of D / 256 waves share each
+// 16-row tile, every wave holding 256 columns of Q and O.
+constexpr int fa_prefill_cgroups(int D) { return D > 256 ? D / 256 : 1; }
+constexpr int fa_prefill_rows(int D) { return 16 * fa_prefill_waves(D) / fa_prefill_cgroups(D); }
 // d = 256: v3 keeps two stages resident and fits its registers only with
-// 16-key stages; v1/v2 (one stage) use 32.
+// 16-key stages; v1/v2 (one stage) use 32.  D > 256: 16-key stages.
 // Low-precision (bf16 / f16) prefill: 128-row workgroups of waves owning MT
 // 16-row tiles each (MT = 1, or 2 for D = 128); 64-key stages.
 constexpr int fa_lp_rows() { return 128; }
 constexpr int fa_lp_waves(int MT) { return fa_lp_rows() / (16 * MT); }
 constexpr int fa_lp_stage_keys() { return 64; }
 constexpr int fa_prefill_stage_keys(int D, int variant) {
-    return D <= 128 ? (fa_prefill_waves(D) == 8 ? 64 : 32) : (variant == 3 ? 16 : 32);
+    return D <= 128 ? (fa_prefill_waves(D) == 8 ? 64 : 32) : (D > 256 || variant == 3 ? 16 : 32);
 }
+// D = 1024: one 16-key stage of K and V takes 130 KiB of LDS, so v3 keeps a
+// single stage (its math is v2's; only the double-buffered schedule goes).
+constexpr int fa_prefill_nbuf(int D, int variant) { return variant == 3 && D <= 512 ? 2 : 1; }
 #endif
 
 #endif

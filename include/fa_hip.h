@@ -37,9 +37,10 @@ extern "C" {
 #define FA_ERR_V_SHAPE 3      /* "v shape mismatch"   src/common.rs:53, :89 */
 #define FA_ERR_OUT_SHAPE 4    /* "out shape mismatch" src/common.rs:54, :90 */
 #define FA_ERR_INVALID_ARG 5  /* NULL pointer with a non-zero length, bad variant/option */
-#define FA_ERR_UNSUPPORTED 6  /* d_head > 256 with 16-bit inputs or a forced path / split
-                                 count, or a size beyond 32-bit row indexing (f32 heads wider
-                                 than 256 on the automatic path run the naive kernels) */
+#define FA_ERR_UNSUPPORTED 6  /* d_head > 256 with 16-bit inputs or a forced split-KV path,
+                                 d_head > 1024 with a forced path / split count, or a size
+                                 beyond 32-bit row indexing (f32 heads up to 1024 run the flash
+                                 kernels; wider ones on the automatic path the naive kernels) */
 #define FA_ERR_NO_DEVICE 7    /* no HIP device visible */
 #define FA_ERR_MODULE 8       /* code object missing / unloadable (FA_HIP_MODULE) */
 #define FA_ERR_ALLOC 9        /* device allocation failed, or the request exceeds the free
@@ -190,7 +191,7 @@ int fa_device_ex(int variant, void* stream, const float* q, const float* k, cons
  * but the split partials (split-KV decode, prefill key split) go to a
  * device-global scratch array of 64 MiB per GPU, held until the process
  * ends, and the call allocates and frees nothing.  Calls whose plan needs a
- * larger workspace return FA_ERR_SCRATCH (out untouched); d_head > 256 (the
+ * larger workspace return FA_ERR_SCRATCH (out untouched); d_head > 1024 (the
  * naive kernels' score matrix) returns FA_ERR_UNSUPPORTED.  Call fa_init()
  * on each device first (it loads the kernels and maps the array; a first
  * call does it itself, which allocates).  All calls on one GPU share its

@@ -47,7 +47,7 @@ int main() {
     // planner sweep
     const size_t bhs[] = {1, 3, 32, 4096};
     const size_t seqs[] = {1, 2, 3, 4, 5, 15, 16, 17, 63, 64, 65, 127, 128, 129, 256, 1000, 2048, 16384, 32768};
-    const size_t ds[] = {1, 3, 4, 8, 17, 31, 32, 33, 64, 100, 127, 128, 129, 200, 255, 256, 257, 512};
+    const size_t ds[] = {1, 3, 4, 8, 17, 31, 32, 33, 64, 100, 127, 128, 129, 200, 255, 256, 257, 512, 513, 1000, 1024, 1025};
     const int splits[] = {0, 1, 2, 3, 16, 1024, 1025};
     char buf[512];
     long plans = 0;

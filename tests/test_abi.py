@@ -252,12 +252,28 @@ def test_planning_key_split_prefill():
 
 
 def test_planning_errors():
-    # f32 heads wider than the flash kernels' 256 columns: the naive kernels
-    # on the automatic path; forced paths and 16-bit inputs are refused
-    assert describe(2, 1, 1, 10, 10, 257, False).startswith("fa_naive_scores_f32")
-    for kw in ({"path": fa.PATH_PREFILL}, {"path": fa.PATH_SPLITKV}, {"dtype": fa.DTYPE_BF16}):
+    # f32 heads of 257..1024 columns: the column-group flash kernels (forced
+    # prefill and key splits too); split-KV and 16-bit inputs stop at 256
+    assert describe(2, 1, 1, 10, 10, 257, False).startswith("fa_prefill_v2_d512_0 grid=1x1x1 block=512")
+    assert describe(3, 1, 4, 1000, 1000, 512, True).startswith("fa_prefill_v3_d512_2 ")
+    assert describe(3, 1, 4, 1000, 1000, 1024, True).startswith("fa_prefill_v3_d1024_1 ")   # one LDS stage
+    assert describe(1, 1, 1, 10, 10, 1000, False).startswith("fa_prefill_v1_d1024_1 ")
+    assert describe(2, 1, 1, 10, 10, 300, False, fa.PATH_PREFILL).startswith("fa_prefill_v2_d512_1 ")
+    s = describe(2, 1, 1, 100, 700, 512, False, fa.PATH_PREFILL, 3)
+    assert s.startswith("fa_prefill_v2_d512_1 ") and "fa_merge_d512" in s and "splits=3" in s
+    assert "fa_merge_d1024" in describe(3, 1, 1, 100, 700, 1024, False, fa.PATH_PREFILL, 3)
+    for kw in ({"path": fa.PATH_SPLITKV}, {"path": fa.PATH_SPLITKV_ROWS}, {"dtype": fa.DTYPE_BF16}):
         with pytest.raises(fa.FaError) as e:
             describe(2, 1, 1, 10, 10, 257, False, **kw)
+        assert e.value.status == fa.FA_ERR_UNSUPPORTED, kw
+    # decode shapes at wide heads stay on the prefill kernels
+    assert describe(2, 1, 32, 1, 32768, 512, False).startswith("fa_prefill_v2_d512_1 ")
+    # wider than 1024: the naive kernels on the automatic path; forced paths
+    # and 16-bit inputs are refused
+    assert describe(2, 1, 1, 10, 10, 1025, False).startswith("fa_naive_scores_f32")
+    for kw in ({"path": fa.PATH_PREFILL}, {"path": fa.PATH_SPLITKV}, {"dtype": fa.DTYPE_BF16}):
+        with pytest.raises(fa.FaError) as e:
+            describe(2, 1, 1, 10, 10, 1025, False, **kw)
         assert e.value.status == fa.FA_ERR_UNSUPPORTED, kw
     with pytest.raises(fa.FaError) as e:
         describe(1, 1, 1, 10, 1000, 64, False, fa.PATH_SPLITKV)

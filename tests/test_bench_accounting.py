@@ -29,6 +29,9 @@ STATED = {   # name: (GFLOP, bytes)
     "config4b": (8.590, 1074266112),
     "config5": (68.719, 167772160),
     "config5c": (8.200, 65536000),
+    # 4 * d * 2048 * 2049 / 2 * heads; Q, K, V, O of heads x 2048 x d f32
+    "wide_d512": (68.753, 268435456),
+    "wide_d1024": (68.753, 268435456),
 }
 
 

@@ -83,11 +83,18 @@ def test_every_padded_head_dim(variant):
         run_case(variant, 70, 90, d, 64, 128, d % 2 == 0)
 
 
+def _wide_kernel(d):
+    return 512 if d <= 512 else 1024
+
+
 @pytest.mark.parametrize("variant", ALL_VARIANTS)
-def test_heads_wider_than_256(variant):
-    # The crate takes any d_head; past the flash kernels' 256 columns the
-    # automatic f32 path runs the naive kernels (materialised scores).
-    for d in (257, 300, 512):
+def test_wide_heads_run_flash_kernels(variant):
+    # The crate's flash path takes any d_head with O(block) scratch
+    # (src/v2.rs:182-189): heads of 257..1024 columns run the column-group
+    # flash kernels (no score matrix), odd widths on the scalar loader.
+    for d in (257, 300, 384, 512, 513, 640, 1000, 1023, 1024):
+        plan = fa.describe_launch(variant, 1, 1, 70, 90, d, d % 2 == 1)
+        assert plan.startswith(f"fa_prefill_v{variant}_d{_wide_kernel(d)}_"), plan
         run_case(variant, 70, 90, d, 64, 128, d % 2 == 1)
     bh, sq, sk, d = 3, 65, 129, 320
     q, k, v = random_vec(bh * sq * d, 4), random_vec(bh * sk * d, 5), random_vec(bh * sk * d, 6)
@@ -102,6 +109,39 @@ def test_heads_wider_than_256(variant):
     want2 = np.concatenate([attention_f64(q2[h * sq * d:(h + 1) * sq * d], k[h * sk * d:(h + 1) * sk * d],
                                           v[h * sk * d:(h + 1) * sk * d], sq, sk, d, True) for h in range(bh)])
     assert max_abs_diff(_device_run(variant, q, k, v, bh, sq, sk, d, True, scale=scale), want2) < 1e-5
+
+
+@pytest.mark.parametrize("d", (384, 512, 1024))
+def test_wide_heads_multiblock_and_key_split(d):
+    """Several query blocks with causal skipping, ragged ends, and the key
+    split (automatic and forced) at wide heads; every variant against CPU v2,
+    v1 / v2 / v3 against each other."""
+    rng = np.random.default_rng(d)
+    for bh, sq, sk, causal in [(2, 300, 300, True), (1, 130, 700, False), (5, 77, 77, True)]:
+        q = rng.standard_normal(bh * sq * d, dtype=np.float32)
+        k = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        v = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+        outs = {}
+        for variant in ALL_VARIANTS:
+            outs[variant] = _device_run(variant, q, k, v, bh, sq, sk, d, causal, guard=64)
+            assert_parity(outs[variant], want, f"v{variant} {bh},{sq},{sk},{d},{causal}")
+        assert_parity(outs[1], outs[2], "v1 vs v2")
+        assert_parity(outs[3], outs[2], "v3 vs v2")
+        for variant in (2, 3):
+            for splits in (2, 3, 5):
+                plan = fa.describe_launch(variant, 1, bh, sq, sk, d, causal, fa.PATH_PREFILL, splits)
+                out = _device_run(variant, q, k, v, bh, sq, sk, d, causal, fa.PATH_PREFILL, splits, guard=64)
+                assert_parity(out, want, f"v{variant} split {splits}: {plan}")
+
+
+@pytest.mark.parametrize("variant", ALL_VARIANTS)
+def test_heads_wider_than_1024_run_naive(variant):
+    # Past the flash kernels' 1024 columns the automatic f32 path runs the
+    # naive kernels (materialised scores, in head chunks capped by free memory).
+    assert fa.describe_launch(variant, 1, 1, 20, 30, 1030, True).startswith("fa_naive_scores_f32")
+    run_case(variant, 20, 30, 1030, 64, 128, True)
+    run_case(variant, 33, 17, 1100, 64, 128, False)
 
 
 @pytest.mark.parametrize("variant", ALL_VARIANTS)
@@ -763,13 +803,13 @@ def test_release_stream_workspace_returns_device_memory():
 
 def test_requests_beyond_device_memory_fail_cleanly():
     """FA_ERR_ALLOC before anything is queued, out untouched, the library
-    usable afterwards: (a) the naive path of a d_head > 256 head whose score
+    usable afterwards: (a) the naive path of a d_head > 1024 head whose score
     matrix (2^19 x 2^19 f32 = 1 TiB) exceeds the device; (b) a forced split
     of 32 heads x 16384 queries x 1024 key splits at d256 (551 GB of
     partials)."""
     torch = _torch()
     dev = torch.device("cuda", 0)
-    n, d = 1 << 19, 300
+    n, d = 1 << 19, 1030
     q = torch.zeros(n * d, device=dev)
     out = torch.full((n * d,), 5.0, device=dev)
     with pytest.raises(fa.FaError) as e:

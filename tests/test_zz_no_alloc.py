@@ -64,6 +64,8 @@ PAIRS = [
     ((3, 8, 16, 8192, 128, False, fa.PATH_AUTO, 0), (2, 2, 5, 900, 64, True, fa.PATH_SPLITKV, 3)),
     # prefill key split: the 16-head 1000 x 1000 d256 causal shape (48 MiB of partials)
     ((3, 16, 1000, 1000, 256, True, fa.PATH_AUTO, 0), (2, 2, 300, 700, 64, False, fa.PATH_PREFILL, 3)),
+    # key split of the column-group kernels for heads wider than 256
+    ((3, 4, 300, 2000, 1024, False, fa.PATH_PREFILL, 4), (2, 2, 100, 700, 512, True, fa.PATH_PREFILL, 3)),
 ]
 
 
@@ -95,9 +97,9 @@ def test_noalloc_refuses_plans_beyond_the_scratch():
         _call(fa.attention_device_noalloc, 2, t, bh, sq, sk, d, False, fa.PATH_SPLITKV, 32)
     assert e.value.status == fa.FA_ERR_SCRATCH
     # d_head beyond the flash kernels (the naive path allocates its score matrix)
-    t = _tensors(1, 8, 8, 300, 10)
+    t = _tensors(1, 8, 8, 1030, 10)
     with pytest.raises(fa.FaError) as e:
-        _call(fa.attention_device_noalloc, 2, t, 1, 8, 8, 300, False, fa.PATH_AUTO, 0)
+        _call(fa.attention_device_noalloc, 2, t, 1, 8, 8, 1030, False, fa.PATH_AUTO, 0)
     assert e.value.status == fa.FA_ERR_UNSUPPORTED
 
 
