@@ -276,8 +276,10 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     const int dtype = opts ? opts->dtype : FA_DTYPE_F32;
     if (dtype != FA_DTYPE_F32 && dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F16) return FA_ERR_INVALID_ARG;
     const bool lp = dtype != FA_DTYPE_F32;   // 16-bit inputs: the fa_prefill_lp kernels
-    if (path < FA_PATH_AUTO || path > FA_PATH_SPLITKV_ROWS) return FA_ERR_INVALID_ARG;
-    if ((path == FA_PATH_SPLITKV || path == FA_PATH_SPLITKV_ROWS) && variant == 1) return FA_ERR_INVALID_ARG;
+    if (path < FA_PATH_AUTO || path > FA_PATH_STREAM) return FA_ERR_INVALID_ARG;
+    if ((path == FA_PATH_SPLITKV || path == FA_PATH_SPLITKV_ROWS || path == FA_PATH_STREAM) && variant == 1)
+        return FA_ERR_INVALID_ARG;
+    if (path == FA_PATH_STREAM && lp) return FA_ERR_UNSUPPORTED;   // f32 kernels only
     if (opts && opts->num_splits < 0) return FA_ERR_INVALID_ARG;
     if (d > (size_t)kMaxD) return FA_ERR_UNSUPPORTED;
     // d_head > 256: f32 prefill kernels only (column groups; key split allowed)
@@ -386,7 +388,34 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
                 return n * bh;
             };
             constexpr double kOverheadKeys = 48.0;
-            if (opts && opts->num_splits > 1 && path == FA_PATH_PREFILL) {
+            // Stream split (f32 v2/v3): the key stages of all (slice, query
+            // block) pairs, slice-major, cut into equal runs of s_per stages,
+            // one run per workgroup (want of them); a block shared by several
+            // runs is merged from one partial per run, kept in block slot
+            // (workgroup + global block index): workgroups + blocks - 1
+            // slots of `rows` rows.  Block b has
+            // R (b + 1) stages while (b + 1) * rows <= seq_k (causal), else
+            // ceil(seq_k / SK); rows is a multiple of SK.
+            size_t s_per = 0, s_wgs = 0, s_segs = 0, s_uhead = 0;
+            auto stream_fit = [&](size_t want) -> bool {
+                const size_t R = rows / SKs, nsf = (sk + SKs - 1) / SKs, bf = sk / rows;
+                const size_t b = nqb;
+                s_uhead = !causal ? b * nsf
+                                  : (b <= bf ? R * (b * (b + 1) / 2) : R * (bf * (bf + 1) / 2) + (b - bf) * nsf);
+                const size_t utot = bh * s_uhead;
+                s_per = std::max<size_t>(4, (utot + want - 1) / want);
+                s_wgs = (utot + s_per - 1) / s_per;
+                s_segs = (max_st + s_per - 1) / s_per + 1;   // most workgroups sharing a block
+                return s_segs <= (size_t)kMaxSplits && s_wgs <= imax && s_uhead <= imax && bh * sq <= imax &&
+                       s_wgs + bh * nqb <= imax;
+            };
+            bool stream = false;
+            if (path == FA_PATH_STREAM) {   // f32 v2/v3 (checked above)
+                if (opts->num_splits > 0 && (size_t)opts->num_splits > imax) return FA_ERR_UNSUPPORTED;
+                if (!stream_fit(opts->num_splits > 0 ? (size_t)opts->num_splits : (size_t)num_cus))
+                    return FA_ERR_UNSUPPORTED;
+                stream = true;
+            } else if (opts && opts->num_splits > 1 && path == FA_PATH_PREFILL) {
                 if (opts->num_splits > kMaxSplits) return FA_ERR_UNSUPPORTED;
                 per = (max_st + opts->num_splits - 1) / opts->num_splits;
             } else if (path == FA_PATH_AUTO && nqb * bh < (size_t)num_cus) {
@@ -412,6 +441,35 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
                         per = pp;
                     }
                 }
+                // The stream split: one round, up to two segment prologues
+                // per workgroup and the merge of the shared blocks.
+                if (!lp && stream_fit((size_t)num_cus)) {
+                    const double cost = (double)s_per * skd + 3.0 * kOverheadKeys;
+                    if (cost < best) {
+                        best = cost;
+                        per = 0;
+                        stream = true;
+                    }
+                }
+            }
+            if (stream) {
+                plan->first.name += "s";   // the stream-split instantiation
+                plan->split = true;
+                p.nqt = static_cast<int>(nqt);
+                p.num_splits = static_cast<int>(s_segs);
+                p.split_len = static_cast<int>(SKs);
+                p.ks_rows = static_cast<int>(rows);
+                p.merge_scale = 1.0f;
+                p.pair_w = 0;
+                p.stream_per = static_cast<long long>(s_per);
+                p.stream_head_units = static_cast<long long>(s_uhead);
+                plan->first.gx = static_cast<unsigned>(s_wgs);
+                std::snprintf(buf, sizeof(buf), "fa_merge_d%d", D);
+                plan->second.name = buf;
+                plan->second.gx = static_cast<unsigned>(bh * sq);   // one wave per output row
+                plan->second.bx = 64;
+                plan->ws_floats = (s_wgs + bh * nqb - 1) * (rows / 16) * (16 * (size_t)D + 32);
+                return FA_OK;
             }
             if (per > 0 && (max_st + per - 1) / per < 2) per = 0;
             if (per > 0 && (bh * sq > imax || per * SKs > imax)) return FA_ERR_UNSUPPORTED;
@@ -646,7 +704,7 @@ int run_device(int variant, hipStream_t stream, const void* q, const void* k, co
         return FA_ERR_ALLOC;   // nothing queued, out untouched
     }
     const int D = pad_d(d);
-    const size_t parts = bh * (size_t)plan.p.nqt * plan.p.num_splits;
+    const size_t parts = plan.ws_floats / (16 * (size_t)D + 32);   // 16-row partials: O, then (m, l)
     plan.p.part_o = ws;
     plan.p.part_ml = ws + parts * 16 * D;
     rc = launch(dev, plan.first, &plan.p, stream);
@@ -1161,7 +1219,10 @@ int fa_describe_launch(int variant, size_t batch, size_t heads, size_t sq, size_
                 std::snprintf(tmp, sizeof(tmp), "; %s grid=%ux%ux%u block=%u; splits=%d", plan.second.name.c_str(),
                               plan.second.gx, plan.second.gy, plan.second.gz, plan.second.bx, plan.p.num_splits);
                 text += tmp;
-                if (plan.p.split_len > 0) {
+                if (plan.p.stream_per > 0) {
+                    std::snprintf(tmp, sizeof(tmp), " stream_per=%lld", plan.p.stream_per);
+                    text += tmp;
+                } else if (plan.p.split_len > 0) {
                     std::snprintf(tmp, sizeof(tmp), " split_len=%d", plan.p.split_len);
                     text += tmp;
                 }

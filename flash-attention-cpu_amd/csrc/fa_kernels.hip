@@ -277,8 +277,17 @@ __device__ __forceinline__ float row4_sum(float x) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-template <int D, int VARIANT, int LOADER>
-__device__ __forceinline__ void prefill_body(const FaParams& p) {
+// One workgroup's share of a query block: query block qb of slice bh (and,
+// in the two-block grid, block qb_second after it), key stages sbeg ..
+// sbeg + nst - 1 of the block's range (nst < 0: to its end); slot >= 0
+// writes a partial (m, l, O) into split slot `slot` for fa_merge, slot < 0
+// the normalised rows.
+struct PrefillSeg {
+    int qb, bh, qb_second, sbeg, nst, slot;
+};
+
+template <int D, int VARIANT, int LOADER, bool OPAQUE_TID = false>
+__device__ __forceinline__ void prefill_segment(const FaParams& p, const PrefillSeg& seg) {
     constexpr int NW = fa_prefill_waves(D);   // waves per workgroup
     constexpr int NT = NW * 64;               // threads
     constexpr int BQ = fa_prefill_rows(D);    // query rows per workgroup
@@ -318,7 +327,11 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     constexpr int XSLOTS = CG > 1 ? (PIPE ? 2 : 1) : 0;
     __shared__ __attribute__((aligned(16))) f32x4 Xs[XSLOTS ? XSLOTS * NW * KB * 64 : 1];
 
-    const int tid = threadIdx.x;
+    int tid = threadIdx.x;
+    // In the stream split's segment loop, an opaque tid keeps per-lane
+    // addresses from being hoisted out of the loop and held in VGPRs across
+    // every stage loop.
+    if constexpr (OPAQUE_TID) asm volatile("" : "+v"(tid));
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int tile = CG > 1 ? wave % TILES : wave;   // the wave's 16-row tile
@@ -327,15 +340,12 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     const int g = lane >> 4;                  // lane group 0..3
     const int li = lane & 15;
 
-    const bool splitk = p.part_o != nullptr;
+    const bool splitk = seg.slot >= 0;
     // two_blocks (v3, no key split): this workgroup runs query blocks
     // nqb-1-r and then r of one (batch, head) -- equal causal work per
     // workgroup, and the second block's loads overlap the first's last step.
-    const bool pairs = VARIANT == 3 && D == 128 && !splitk && p.two_blocks != 0;
-    int qb, bh, ysplit = 0, qb_second = 0;
-    if (splitk) map_block_split(p, qb, bh, ysplit);
-    else if (pairs) map_pair(p, blockIdx.x, qb, qb_second, bh);
-    else map_block(p, blockIdx.x, qb, bh);
+    const bool pairs = VARIANT == 3 && D == 128 && seg.qb_second >= 0;
+    const int qb = seg.qb, bh = seg.bh, ysplit = seg.slot, qb_second = seg.qb_second;
     const int seq_q = p.seq_q, seq_k = p.seq_k, d = p.d;
     int q0 = qb * BQ;
     const float* __restrict__ Qh = p.q + (size_t)bh * seq_q * d;
@@ -381,15 +391,12 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     // (src/v2.rs:208-212, src/v3.rs:396-410).
     auto block_end = [&](int q0_) { return (VARIANT != 1 && causal) ? min(seq_k, q0_ + BQ) : seq_k; };
     int kend = block_end(q0);
-    // Key split (v2/v3 on grids smaller than the GPU): the workgroup for
-    // split y takes the split_len keys from y * split_len of its block's
-    // range and writes a partial (m, l, O) that fa_merge combines.
-    int sbeg = 0, nst = (kend + SK - 1) / SK;
-    if (splitk) {
-        const int per = p.split_len / SK;
-        sbeg = ysplit * per;              // < nst by construction of the grid
-        nst = min(nst, sbeg + per) - sbeg;
-    }
+    // Key split / stream split (v2/v3 on grids smaller than the GPU): this
+    // workgroup takes stages sbeg .. sbeg + nst - 1 of the block's range
+    // (sbeg < the block's stage count by construction of the grid).
+    const int sbeg = seg.sbeg;
+    int nst = (kend + SK - 1) / SK - sbeg;
+    if (seg.nst >= 0) nst = min(nst, seg.nst);
     const int k0 = sbeg * SK;                 // first key of this workgroup
 
     // ---- stage loaders ------------------------------------------------------
@@ -980,7 +987,10 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
         const int qt = q0 / 16 + tile;
         if (qt >= p.nqt) return;
         const float lt = row4_sum(l);
-        const size_t pidx = ((size_t)bh * p.nqt + qt) * p.num_splits + ysplit;
+        // key split: slot (bh, qt, split); stream split: the block slot
+        // (workgroup + global block index) times the block's 16-row tiles
+        const size_t pidx = p.stream_per > 0 ? (size_t)ysplit * TILES + tile
+                                             : ((size_t)bh * p.nqt + qt) * p.num_splits + ysplit;
         float* po = p.part_o + pidx * 16 * D;
         float* pml = p.part_ml + pidx * 32;
         if (g == 0 && cgrp == 0) {   // (m, l) agree across the column group
@@ -999,6 +1009,124 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
     }
 
     write_out();
+}
+
+// Stream split ("stream-K"): the (slice, query block, key stage) units of a
+// v2/v3 prefill, slice-major and block-major, are cut into equal runs of
+// p.stream_per units, one per workgroup, so every workgroup has the same
+// number of stages however unequal the causal blocks are.  A run may end
+// inside one block and start the next; each piece is a segment.  A block
+// covered by one workgroup is written directly; a block shared by several
+// gets one partial per workgroup and fa_merge combines them.  The partial of
+// workgroup w for global block bg (slice * nqb + block) sits in block slot
+// w + bg: a block's workgroups are consecutive and the last workgroup of a
+// block is at most the first of the next, so slots never collide, and
+// (workgroups + blocks - 1) slots of BQ rows hold them all.  Stage counts per block follow from
+// BQ % SK == 0: block b has R (b + 1) stages (R = BQ / SK) while BQ (b + 1)
+// <= seq_k (causal), otherwise ceil(seq_k / SK).
+struct StreamGeom {
+    long long R, nsf, bf, u_head;
+    bool causal;
+};
+__device__ __forceinline__ StreamGeom stream_geom(const FaParams& p, int bq, int sk_stage) {
+    StreamGeom g;
+    g.R = bq / sk_stage;
+    g.nsf = (p.seq_k + sk_stage - 1) / sk_stage;
+    g.bf = p.seq_k / bq;
+    g.causal = p.causal != 0;
+    g.u_head = p.stream_head_units;
+    return g;
+}
+// units of slice-local blocks 0 .. b-1
+__device__ __forceinline__ long long stream_prefix(const StreamGeom& g, long long b) {
+    if (!g.causal) return b * g.nsf;
+    if (b <= g.bf) return g.R * (b * (b + 1) / 2);
+    return g.R * (g.bf * (g.bf + 1) / 2) + (b - g.bf) * g.nsf;
+}
+__device__ __forceinline__ long long stream_stages(const StreamGeom& g, long long b) {
+    return (g.causal && b < g.bf) ? g.R * (b + 1) : g.nsf;
+}
+// the block holding slice-local unit r
+__device__ __forceinline__ long long stream_block(const StreamGeom& g, long long r) {
+    if (!g.causal) return r / g.nsf;
+    const long long tri = g.R * (g.bf * (g.bf + 1) / 2);
+    if (r >= tri) return g.bf + (r - tri) / g.nsf;
+    long long b = (long long)((sqrtf(8.0f * (float)(r / g.R) + 1.0f) - 1.0f) * 0.5f);
+    while (b > 0 && stream_prefix(g, b) > r) --b;
+    while (stream_prefix(g, b + 1) <= r) ++b;
+    return b;
+}
+// workgroups first .. last share block b of slice h (units [ub, ub + n))
+__device__ __forceinline__ void stream_span(const StreamGeom& g, long long per, long long h, long long b,
+                                            long long& first, long long& last) {
+    const long long ub = h * g.u_head + stream_prefix(g, b);
+    first = ub / per;
+    last = (ub + stream_stages(g, b) - 1) / per;
+}
+
+// STREAM: the stream-split instantiation (a loop over segments); the others
+// run one segment, so their stage loops keep the registers a loop around
+// them would take (per-lane addresses hoisted out of it stay live).
+template <int D, int VARIANT, int LOADER, bool STREAM>
+__device__ __forceinline__ void prefill_body(const FaParams& p) {
+    constexpr int BQ = fa_prefill_rows(D);
+    constexpr int SK = fa_prefill_stage_keys(D, VARIANT);
+    static_assert(BQ % SK == 0, "stream split: whole stages per block");
+    static_assert(!STREAM || VARIANT != 1, "v1 never splits its keys");
+    const bool stream = STREAM;
+    // Loop state kept in SGPRs (readfirstlane): it is live across every
+    // segment's stage loop, where VGPRs are short.  Unit indices fit 32 bits
+    // (the host checks the total).
+    int u = 0, uend = 0, wg = 0;
+    if (stream) {
+        // Workgroups are dispatched round-robin over the 8 XCDs: consecutive
+        // runs (mostly one slice's blocks) go to the same XCD, whose L2 then
+        // holds that slice's K / V.
+        const int G = gridDim.x;
+        const int x = blockIdx.x;
+        wg = (G % 8 == 0) ? (x % 8) * (G / 8) + x / 8 : x;
+        const long long per = p.stream_per;
+        u = (int)(wg * per);
+        uend = (int)min((long long)wg * per + per, (long long)p.bh * p.stream_head_units);
+    }
+    for (int it = 0;; ++it) {
+        u = __builtin_amdgcn_readfirstlane(u);
+        uend = __builtin_amdgcn_readfirstlane(uend);
+        wg = __builtin_amdgcn_readfirstlane(wg);
+        PrefillSeg seg{0, 0, -1, 0, -1, -1};
+        if (stream) {
+            if (u >= uend) break;
+            const StreamGeom sg = stream_geom(p, BQ, SK);
+            const long long h = u / sg.u_head, r = u % sg.u_head;
+            const long long b = stream_block(sg, r);
+            const long long s0 = r - stream_prefix(sg, b);
+            const long long cnt = min(stream_stages(sg, b) - s0, (long long)(uend - u));
+            long long first, last;
+            stream_span(sg, p.stream_per, h, b, first, last);
+            seg.qb = (int)b;
+            seg.bh = (int)h;
+            seg.sbeg = (int)s0;
+            seg.nst = (int)cnt;
+            seg.slot = first == last ? -1 : (int)(wg + h * p.nqb + b);
+            u += (int)cnt;
+        } else {
+            if (it > 0) break;
+            if (p.part_o != nullptr) {
+                int y;
+                map_block_split(p, seg.qb, seg.bh, y);
+                seg.slot = y;
+                seg.sbeg = y * (p.split_len / SK);
+                seg.nst = p.split_len / SK;
+            } else if (VARIANT == 3 && D == 128 && p.two_blocks != 0) {
+                map_pair(p, blockIdx.x, seg.qb, seg.qb_second, seg.bh);
+            } else {
+                map_block(p, blockIdx.x, seg.qb, seg.bh);
+            }
+        }
+        // (the opaque tid spills at D >= 512 and is not needed there)
+        prefill_segment<D, VARIANT, LOADER, STREAM && D <= 256>(p, seg);
+        if (stream) __syncthreads();   // LDS stages and slots are reused by the next segment
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1268,23 +1396,36 @@ __device__ __forceinline__ void merge_body(const FaParams& p) {
     const int q = row % p.seq_q, bh = row / p.seq_q;
     const int qt = q / 16, qi = q % 16;
     const float c = p.merge_scale;   // partial maxima -> log2 domain
-    const size_t pbase = ((size_t)bh * p.nqt + qt) * p.num_splits;
+    // Partial sp of this row's 16-row tile: pbase + sp * pstride.
+    size_t pbase = ((size_t)bh * p.nqt + qt) * p.num_splits, pstride = 1;
     // Splits holding data for this row: all of them for split-KV; for the
     // prefill key split, those starting below the row's block key end.
     int ns = p.num_splits;
-    if (p.ks_rows > 0) {
+    if (p.stream_per > 0) {
+        // stream split (split_len = the stage, ks_rows = the block): the
+        // workgroups first .. last sharing this row's block (one: it wrote
+        // the row), whose partials sit in block slots w + bh * nqb + block
+        const StreamGeom sg = stream_geom(p, p.ks_rows, p.split_len);
+        const int blk = q / p.ks_rows;
+        long long first, last;
+        stream_span(sg, p.stream_per, bh, blk, first, last);
+        if (first == last) return;
+        ns = (int)(last - first + 1);
+        pstride = (size_t)(p.ks_rows / 16);
+        pbase = ((size_t)first + (size_t)bh * p.nqb + blk) * pstride + (q % p.ks_rows) / 16;
+    } else if (p.ks_rows > 0) {
         const int kend = p.causal ? min(p.seq_k, (q / p.ks_rows + 1) * p.ks_rows) : p.seq_k;
         ns = min(ns, (kend + p.split_len - 1) / p.split_len);
     }
 
     float M = FA_NEG_INF;
-    for (int sp = lane; sp < ns; sp += 64) M = fmaxf(M, p.part_ml[(pbase + sp) * 32 + qi]);
+    for (int sp = lane; sp < ns; sp += 64) M = fmaxf(M, p.part_ml[(pbase + sp * pstride) * 32 + qi]);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
     const float Mu = (M == FA_NEG_INF) ? 0.0f : M;
     float L = 0.0f;
     for (int sp = lane; sp < ns; sp += 64) {
-        const float* ml = p.part_ml + (pbase + sp) * 32;
+        const float* ml = p.part_ml + (pbase + sp * pstride) * 32;
         const float w = rescale_factor(ml[qi], Mu, c);
         wts[sp] = w;
         L += ml[16 + qi] * w;
@@ -1304,7 +1445,7 @@ __device__ __forceinline__ void merge_body(const FaParams& p) {
             const float w = wts[sp];
 #pragma unroll
             for (int cc = 0; cc < CPL; ++cc)
-                acc[cc] += *reinterpret_cast<const f32x4*>(po + (size_t)sp * 16 * D + 256 * cc) * w;
+                acc[cc] += *reinterpret_cast<const f32x4*>(po + sp * pstride * 16 * D + 256 * cc) * w;
         }
         const float inv = L > 0.0f ? 1.0f / L : 0.0f;
         float* orow = p.out + (size_t)row * p.d;
@@ -1323,7 +1464,7 @@ __device__ __forceinline__ void merge_body(const FaParams& p) {
         const float* po = p.part_o + (pbase * 16 + qi) * D + 4 * ch;
 #pragma unroll 8
         for (int sp = grp; sp < ns; sp += GROUPS)
-            acc += *reinterpret_cast<const f32x4*>(po + (size_t)sp * 16 * D) * wts[sp];
+            acc += *reinterpret_cast<const f32x4*>(po + sp * pstride * 16 * D) * wts[sp];
     }
     if constexpr (GROUPS > 1) {
         *reinterpret_cast<f32x4*>(part + 4 * lane) = acc;
@@ -1512,11 +1653,17 @@ __device__ __forceinline__ void naive_pv_body(const NaiveParams& p) {
 // ---------------------------------------------------------------------------
 // Named entry points for hipModuleGetFunction.
 // ---------------------------------------------------------------------------
-// fa_prefill_v{V}_d{D}_{L}: L = 0 scalar loads, 1 vector loads, 2 LDS DMA (v3).
+// fa_prefill_v{V}_d{D}_{L}: L = 0 scalar loads, 1 vector loads, 2 LDS DMA (v3);
+// fa_prefill_v{V}_d{D}_{L}s: the stream split (v2 / v3).
 #define FA_PREFILL(D, VAR, LD)                                                                   \
     extern "C" __global__ void __launch_bounds__(64 * fa_prefill_waves(D), 8 / fa_prefill_waves(D))   \
         fa_prefill_v##VAR##_d##D##_##LD(FaParams p) {                                                \
-        prefill_body<D, VAR, LD>(p);                                                             \
+        prefill_body<D, VAR, LD, false>(p);                                                      \
+    }
+#define FA_PREFILL_S(D, VAR, LD)                                                                 \
+    extern "C" __global__ void __launch_bounds__(64 * fa_prefill_waves(D), 8 / fa_prefill_waves(D))   \
+        fa_prefill_v##VAR##_d##D##_##LD##s(FaParams p) {                                             \
+        prefill_body<D, VAR, LD, true>(p);                                                       \
     }
 #define FA_PREFILL_ALL(D)  \
     FA_PREFILL(D, 1, 0)    \
@@ -1525,7 +1672,12 @@ __device__ __forceinline__ void naive_pv_body(const NaiveParams& p) {
     FA_PREFILL(D, 2, 1)    \
     FA_PREFILL(D, 3, 0)    \
     FA_PREFILL(D, 3, 1)    \
-    FA_PREFILL(D, 3, 2)
+    FA_PREFILL(D, 3, 2)    \
+    FA_PREFILL_S(D, 2, 0)  \
+    FA_PREFILL_S(D, 2, 1)  \
+    FA_PREFILL_S(D, 3, 0)  \
+    FA_PREFILL_S(D, 3, 1)  \
+    FA_PREFILL_S(D, 3, 2)
 
 FA_PREFILL_ALL(32)
 FA_PREFILL_ALL(64)
@@ -1539,6 +1691,10 @@ FA_PREFILL(1024, 2, 0)
 FA_PREFILL(1024, 2, 1)
 FA_PREFILL(1024, 3, 0)
 FA_PREFILL(1024, 3, 1)
+FA_PREFILL_S(1024, 2, 0)
+FA_PREFILL_S(1024, 2, 1)
+FA_PREFILL_S(1024, 3, 0)
+FA_PREFILL_S(1024, 3, 1)
 
 // Decode register double-buffering (FA_DECODE_DBUF=1) trades occupancy for
 // one block of loads in flight per register set.

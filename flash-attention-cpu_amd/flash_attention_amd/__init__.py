@@ -51,6 +51,7 @@ PATH_AUTO = 0
 PATH_PREFILL = 1
 PATH_SPLITKV = 2
 PATH_SPLITKV_ROWS = 3
+PATH_STREAM = 4
 
 NAIVE_F32 = 0
 NAIVE_F64 = 1

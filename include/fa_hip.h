@@ -162,13 +162,19 @@ int fa_release_stream_workspace(void* stream);
  * merged), FA_PATH_SPLITKV (16-row decode tiles, always split; v2/v3 only),
  * FA_PATH_SPLITKV_ROWS (row-streaming split-KV for seq_len_q <= 4: K and V
  * read as whole rows, dot products on the vector ALUs; v2/v3, f32, d_head %
- * 4 == 0 and 16-byte aligned operands, else FA_ERR_UNSUPPORTED).  AUTO picks
- * the row-streaming kernel for decode shapes it supports.
+ * 4 == 0 and 16-byte aligned operands, else FA_ERR_UNSUPPORTED),
+ * FA_PATH_STREAM (query-block kernel with the stream split: the key stages
+ * of every (slice, query block) cut into equal runs, one per workgroup --
+ * num_splits workgroups, 0 = one per CU -- with partials merged where a
+ * block is shared; v2/v3, f32).  AUTO picks the row-streaming kernel for
+ * decode shapes it supports and the stream split or the key split for
+ * prefills smaller than the GPU.
  * num_splits = 0 lets the library choose (at most 1024). */
 #define FA_PATH_AUTO 0
 #define FA_PATH_PREFILL 1
 #define FA_PATH_SPLITKV 2
 #define FA_PATH_SPLITKV_ROWS 3
+#define FA_PATH_STREAM 4
 /* Element type of Q, K, V (O is always f32). */
 #define FA_DTYPE_F32 0
 #define FA_DTYPE_BF16 1

@@ -235,9 +235,29 @@ def test_planning_split_kv():
     assert describe(3, 1, 1, 256, 256, 64, False, dtype=fa.DTYPE_BF16).startswith("fa_prefill_lp_bf16")
 
 
-def test_planning_key_split_prefill():
-    # config 5c: 8 query blocks x 16 heads = 128 workgroups < 256 CUs
+def test_planning_stream_split_prefill():
+    # config 5c: 8 query blocks x 16 heads = 128 workgroups < 256 CUs; v3's
+    # 16-key stages: blocks of 8, 16, ..., 56 and 63 stages, 287 per head,
+    # 4592 in all -> runs of 18 over 256 workgroups; block slots = 256 + 128 - 1
+    # of 8 tiles x (16 x 256 + 32) floats
     s = describe(3, 1, 16, 1000, 1000, 256, True)
+    assert s.startswith("fa_prefill_v3_d256_2s grid=256x1x1 block=512; fa_merge_d256 grid=16000x1x1 block=64; ")
+    assert "stream_per=18" in s and f"workspace={(256 + 128 - 1) * 8 * (16 * 256 + 32) * 4}" in s
+    # v2's 32-key stages: 4 + 8 + ... + 28 + 32 = 144 per head -> runs of 9
+    assert "grid=256x1x1" in describe(2, 1, 16, 1000, 1000, 256, True) and \
+        "stream_per=9" in describe(2, 1, 16, 1000, 1000, 256, True)
+    # forced: the workgroup count, at least 4 stages per run
+    assert describe(3, 1, 16, 1000, 1000, 256, True, fa.PATH_STREAM, 100).startswith("fa_prefill_v3_d256_2s grid=100x1x1")
+    assert "stream_per=46" in describe(3, 1, 16, 1000, 1000, 256, True, fa.PATH_STREAM, 100)
+    assert "stream_per=4" in describe(2, 1, 1, 256, 256, 64, False, fa.PATH_STREAM)   # 4 stages: one run
+    with pytest.raises(fa.FaError) as e:
+        describe(2, 1, 1, 256, 256, 64, False, fa.PATH_STREAM, dtype=fa.DTYPE_BF16)
+    assert e.value.status == fa.FA_ERR_UNSUPPORTED
+
+
+def test_planning_key_split_prefill():
+    # config 5c's shape, split forced over 3 workgroups per block
+    s = describe(3, 1, 16, 1000, 1000, 256, True, fa.PATH_PREFILL, 3)
     assert s.startswith("fa_prefill_v3_d256_2 grid=") and "fa_merge_d256 grid=16000x1x1" in s
     nks, split_len = int(s.split("splits=")[1].split()[0]), int(s.split("split_len=")[1].split()[0])
     assert split_len % 16 == 0 and nks * split_len >= 1000 > (nks - 1) * split_len
@@ -256,7 +276,7 @@ def test_planning_errors():
     # prefill and key splits too); split-KV and 16-bit inputs stop at 256
     assert describe(2, 1, 1, 10, 10, 257, False).startswith("fa_prefill_v2_d512_0 grid=1x1x1 block=512")
     assert describe(3, 1, 4, 1000, 1000, 512, True).startswith("fa_prefill_v3_d512_2 ")
-    assert describe(3, 1, 4, 1000, 1000, 1024, True).startswith("fa_prefill_v3_d1024_1 ")   # one LDS stage
+    assert describe(3, 1, 4, 1000, 1000, 1024, True).startswith("fa_prefill_v3_d1024_1s ")   # one LDS stage
     assert describe(1, 1, 1, 10, 10, 1000, False).startswith("fa_prefill_v1_d1024_1 ")
     assert describe(2, 1, 1, 10, 10, 300, False, fa.PATH_PREFILL).startswith("fa_prefill_v2_d512_1 ")
     s = describe(2, 1, 1, 100, 700, 512, False, fa.PATH_PREFILL, 3)

@@ -500,6 +500,36 @@ def test_key_split_prefill_matches_oracle():
             assert_parity(a, want, f"auto v{variant} {bh},{sq},{sk},{d},{causal}")
 
 
+def test_stream_split_prefill_matches_oracle():
+    """v2/v3 query-block kernel with the stream split: the key stages of all
+    (slice, query block) pairs cut into equal runs, one per workgroup, runs
+    crossing block and slice boundaries, shared blocks merged (forced here
+    with several workgroup counts; chosen automatically for small causal
+    grids such as config 5c).  Ragged ends, non-causal, seq_q > seq_k, every
+    kernel width."""
+    rng = np.random.default_rng(79)
+    cases = [(16, 1000, 1000, 256, True), (3, 300, 700, 64, False), (2, 700, 300, 128, True),
+             (3, 129, 1025, 32, True), (1, 257, 513, 17, False), (2, 600, 600, 512, True), (1, 100, 900, 1024, True),
+             (5, 77, 77, 128, True)]
+    for bh, sq, sk, d, causal in cases:
+        q = rng.standard_normal(bh * sq * d, dtype=np.float32)
+        k = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        v = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+        for splits in (0, 1, 3, 7, 64):
+            for variant in (2, 3):
+                plan = fa.describe_launch(variant, 1, bh, sq, sk, d, causal, fa.PATH_STREAM, splits)
+                tag = f"stream v{variant} workgroups={splits} {bh},{sq},{sk},{d},{causal}: {plan}"
+                print("[case]", tag, flush=True)
+                assert "stream_per=" in plan, tag
+                got = _device_run(variant, q, k, v, bh, sq, sk, d, causal, fa.PATH_STREAM, splits, guard=64)
+                assert_parity(got, want, tag)
+    with pytest.raises(fa.FaError) as e:
+        fa.describe_launch(1, 1, 16, 1000, 1000, 256, True, fa.PATH_STREAM)
+    assert e.value.status == fa.FA_ERR_INVALID_ARG   # v1 never splits its keys
+    assert "stream_per=18" in fa.describe_launch(3, 1, 16, 1000, 1000, 256, True)   # config 5c: automatic
+
+
 def test_two_block_workgroups_match_oracle():
     """f32 v3 grids whose block pairs fill whole rounds of the GPU run query
     blocks nqb-1-r and r in one workgroup, the second block's loads issued

@@ -1,0 +1,124 @@
+"""The stream split's index arithmetic, checked on the CPU.
+
+The prefill kernel (prefill_body in csrc/fa_kernels.hip) cuts the key stages
+of every (slice, query block) into equal runs, one per workgroup, and each
+run into segments; fa_merge finds the partials of a shared block again.
+This test walks the same arithmetic in Python for many shapes and checks the
+invariants the kernels rely on, against brute-force enumeration:
+
+* every (slice, block, stage) unit is processed exactly once, and the
+  per-block stage counts equal ceil(block key end / SK) (causal: the block's
+  last row + 1, capped at seq_k; the reference's causal tile skip,
+  src/v2.rs:208-212);
+* the closed-form block lookup (with its float square-root estimate) agrees
+  with a linear search;
+* a block touched by one workgroup is written directly; the partial slots
+  (workgroup + global block) are unique and below the slot count the host
+  allocates, and the merge's slots for a block are exactly those written;
+* the workgroups sharing one block never exceed the host's slot bound.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+
+def geom(sk, bq, skk, causal):
+    return {"R": bq // skk, "nsf": -(-sk // skk), "bf": sk // bq, "causal": causal}
+
+
+def prefix(g, b):
+    if not g["causal"]:
+        return b * g["nsf"]
+    if b <= g["bf"]:
+        return g["R"] * (b * (b + 1) // 2)
+    return g["R"] * (g["bf"] * (g["bf"] + 1) // 2) + (b - g["bf"]) * g["nsf"]
+
+
+def stages(g, b):
+    return g["R"] * (b + 1) if (g["causal"] and b < g["bf"]) else g["nsf"]
+
+
+def block_of(g, r):
+    if not g["causal"]:
+        return r // g["nsf"]
+    tri = g["R"] * (g["bf"] * (g["bf"] + 1) // 2)
+    if r >= tri:
+        return g["bf"] + (r - tri) // g["nsf"]
+    b = int((np.sqrt(np.float32(8.0) * np.float32(r // g["R"]) + np.float32(1.0)) - np.float32(1.0))
+            * np.float32(0.5))
+    while b > 0 and prefix(g, b) > r:
+        b -= 1
+    while prefix(g, b + 1) <= r:
+        b += 1
+    return b
+
+
+def plan(bh, sq, sk, bq, skk, causal, want):
+    """Host side (make_plan's stream_fit)."""
+    nqb = -(-sq // bq)
+    g = geom(sk, bq, skk, causal)
+    u_head = prefix(g, nqb)
+    utot = bh * u_head
+    per = max(4, -(-utot // want))
+    wgs = -(-utot // per)
+    max_st = -(-(min(sk, nqb * bq) if causal else sk) // skk)
+    segs = -(-max_st // per) + 1
+    slots = wgs + bh * nqb - 1
+    return g, nqb, u_head, per, wgs, segs, slots
+
+
+CASES = [
+    # bh, sq, sk, rows per block, stage keys, causal, workgroups wanted
+    (16, 1000, 1000, 128, 16, True, 256), (16, 1000, 1000, 128, 32, True, 256), (3, 300, 300, 64, 16, True, 256),
+    (1, 256, 256, 128, 64, False, 256), (4, 2048, 2048, 128, 64, True, 256), (2, 2000, 700, 128, 64, True, 100),
+    (5, 77, 5000, 32, 16, True, 7), (7, 129, 129, 128, 64, True, 3), (1, 5000, 130, 128, 64, True, 256),
+    (2, 1000, 1000, 128, 16, False, 1000), (9, 640, 1000, 64, 16, True, 256), (1, 1, 1, 128, 64, True, 256),
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_stream_split_covers_every_unit_once(case):
+    bh, sq, sk, bq, skk, causal, want = case
+    g, nqb, u_head, per, wgs, segs, slots = plan(bh, sq, sk, bq, skk, causal, want)
+    for b in range(nqb):   # stage counts and prefix sums against brute force
+        kend = min(sk, (b + 1) * bq) if causal else sk
+        assert stages(g, b) == -(-kend // skk)
+        assert prefix(g, b) == sum(stages(g, x) for x in range(b))
+    for r in range(u_head):
+        b = max(x for x in range(nqb) if prefix(g, x) <= r)
+        assert block_of(g, r) == b, r
+    seen = np.zeros(bh * u_head, np.int32)
+    written = {}           # (h, b) -> list of slots, or "direct"
+    used_slots = set()
+    for wg in range(wgs):
+        u, uend = wg * per, min(wg * per + per, bh * u_head)
+        while u < uend:
+            h, r = divmod(u, u_head)
+            b = block_of(g, r)
+            s0 = r - prefix(g, b)
+            cnt = min(stages(g, b) - s0, uend - u)
+            ub = h * u_head + prefix(g, b)
+            first, last = ub // per, (ub + stages(g, b) - 1) // per
+            seen[u:u + cnt] += 1
+            if first == last:
+                assert s0 == 0 and cnt == stages(g, b)
+                written[(h, b)] = "direct"
+            else:
+                slot = wg + h * nqb + b
+                assert 0 <= slot < slots and slot not in used_slots
+                used_slots.add(slot)
+                written.setdefault((h, b), []).append(slot)
+                assert last - first + 1 <= segs
+            u += cnt
+    assert np.all(seen == 1)
+    for h in range(bh):
+        for b in range(nqb):
+            ub = h * u_head + prefix(g, b)
+            first, last = ub // per, (ub + stages(g, b) - 1) // per
+            if first == last:
+                assert written[(h, b)] == "direct"
+            else:   # fa_merge's slots: first + j + h * nqb + b, j < last - first + 1
+                assert sorted(written[(h, b)]) == [first + j + h * nqb + b for j in range(last - first + 1)]
