@@ -541,7 +541,8 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
         std::snprintf(buf, sizeof(buf), "fa_decode_%s_d%d_%d", dtype == FA_DTYPE_BF16 ? "bf16" : "f16", D,
                       vec8 ? 1 : 0);
     } else {
-        std::snprintf(buf, sizeof(buf), "fa_decode_d%d_%d", D, vec ? 1 : 0);
+        // 0: scalar loads, 1: 16-byte loads, 2: K through per-wave LDS rings (D = 64, 128)
+        std::snprintf(buf, sizeof(buf), "fa_decode_d%d_%d", D, vec ? (D == 64 || D == 128 ? 2 : 1) : 0);
     }
     plan->first.name = buf;
     plan->first.gx = static_cast<unsigned>(nsplit);

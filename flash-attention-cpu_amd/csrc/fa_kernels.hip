@@ -56,6 +56,11 @@ constexpr float kLazyMax = 8.0f;
 #ifndef FA_DECODE_INTERLEAVE
 #define FA_DECODE_INTERLEAVE 1
 #endif
+// Cache policy of the decode K DMA (buffer aux bits): 2 = nt, the stream is
+// read once (measured on config 4b: 168.1 -> 162.8 us against 0).
+#ifndef FA_DECODE_KLDS_AUX
+#define FA_DECODE_KLDS_AUX 2
+#endif
 // v3 prefill: only the upper half of the waves issue the stage DMA.
 #ifndef FA_FILL_HALF
 #define FA_FILL_HALF 1
@@ -286,7 +291,7 @@ struct PrefillSeg {
     int qb, bh, qb_second, sbeg, nst, slot;
 };
 
-template <int D, int VARIANT, int LOADER, bool OPAQUE_TID = false>
+template <int D, int VARIANT, int LOADER, bool STREAM, bool OPAQUE_TID>
 __device__ __forceinline__ void prefill_segment(const FaParams& p, const PrefillSeg& seg) {
     constexpr int NW = fa_prefill_waves(D);   // waves per workgroup
     constexpr int NT = NW * 64;               // threads
@@ -340,11 +345,12 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
     const int g = lane >> 4;                  // lane group 0..3
     const int li = lane & 15;
 
-    const bool splitk = seg.slot >= 0;
+    // key split: the launch has partials; stream split: this segment's block is shared
+    const bool splitk = STREAM ? seg.slot >= 0 : p.part_o != nullptr;
     // two_blocks (v3, no key split): this workgroup runs query blocks
     // nqb-1-r and then r of one (batch, head) -- equal causal work per
     // workgroup, and the second block's loads overlap the first's last step.
-    const bool pairs = VARIANT == 3 && D == 128 && seg.qb_second >= 0;
+    const bool pairs = !STREAM && VARIANT == 3 && D == 128 && !splitk && p.two_blocks != 0;
     const int qb = seg.qb, bh = seg.bh, ysplit = seg.slot, qb_second = seg.qb_second;
     const int seq_q = p.seq_q, seq_k = p.seq_k, d = p.d;
     int q0 = qb * BQ;
@@ -989,8 +995,8 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
         const float lt = row4_sum(l);
         // key split: slot (bh, qt, split); stream split: the block slot
         // (workgroup + global block index) times the block's 16-row tiles
-        const size_t pidx = p.stream_per > 0 ? (size_t)ysplit * TILES + tile
-                                             : ((size_t)bh * p.nqt + qt) * p.num_splits + ysplit;
+        const size_t pidx = STREAM ? (size_t)ysplit * TILES + tile
+                                   : ((size_t)bh * p.nqt + qt) * p.num_splits + ysplit;
         float* po = p.part_o + pidx * 16 * D;
         float* pml = p.part_ml + pidx * 32;
         if (g == 0 && cgrp == 0) {   // (m, l) agree across the column group
@@ -1124,7 +1130,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
             }
         }
         // (the opaque tid spills at D >= 512 and is not needed there)
-        prefill_segment<D, VARIANT, LOADER, STREAM && D <= 256>(p, seg);
+        prefill_segment<D, VARIANT, LOADER, STREAM, STREAM && D <= 256>(p, seg);
         if (stream) __syncthreads();   // LDS stages and slots are reused by the next segment
     }
 }
@@ -1146,16 +1152,36 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
 // ---------------------------------------------------------------------------
 // E: element type of Q/K/V (float, or bf16 / f16 widened to f32 as loaded).
 // DBUF_REQ: double-buffer the K/V registers; D = 256 has no registers for it.
-template <int D, bool VEC, bool DBUF_REQ, typename E = float>
+// KLDS (f32, 16-byte aligned operands, d % 4 == 0, D = 64, 128): K reaches
+// the MFMA through LDS.  Each wave keeps a two-slot ring of its own 16-key
+// blocks in LDS, filled by global->LDS DMA in whole padded rows (D + 8
+// floats, written as 1 KiB runs: one wave-wide load covers about two
+// contiguous K rows), and reads the A operand from there; V stays in
+// registers.  The MFMA-layout K loads of the register path touch 16 rows x
+// 64 bytes per instruction (measured: 5.7-6.1 TB/s for that pattern against
+// 6.4-6.9 TB/s for whole rows).  No barriers: a wave only reads its own
+// slots, after s_waitcnt on its own DMA.
+template <int D, bool VEC, bool DBUF_REQ, typename E = float, bool KLDS = false>
 __device__ __forceinline__ void decode_body(const FaParams& p) {
     constexpr bool DBUF = DBUF_REQ && D <= 128;
+    static_assert(!KLDS || (DBUF && VEC && D >= 64 && std::is_same<E, float>::value),
+                  "LDS-staged K: f32, vector loads, 4 V columns per lane");
     constexpr int NQ = D / 4;          // MFMA k-steps over d (16x16x4)
     constexpr int NKL = D / 16;        // 128-bit K loads per lane per 16 keys
     constexpr int NVL = D / 64 > 0 ? D / 64 : 1;  // 128-bit V loads per lane per key step
     constexpr int VW = D >= 64 ? 4 : D / 16;      // floats per lane per V load
     constexpr int NOB = D / 16;        // O^T blocks of 16 dv
     constexpr int WSTRIDE = NOB * 4 * 64 + 128;
-    __shared__ __attribute__((aligned(16))) float lds[3 * WSTRIDE];
+    constexpr int KLD = D + 8;                 // padded K row in LDS (floats)
+    constexpr int KCH = KLD / 4;               // 16-byte chunks per padded row
+    constexpr int KTOT = 16 * KCH;             // chunks per 16-key block image
+    constexpr int KRUNS = (KTOT + 63) / 64;    // 1 KiB DMA runs per block
+    constexpr int KIMG = KRUNS * 256;          // floats per wave slot (whole 1 KiB runs)
+    static_assert(!KLDS || 4 * KIMG >= 3 * WSTRIDE, "merge area inside slot 0");
+    __shared__ __attribute__((aligned(16))) float lds[KLDS ? 1 : 3 * WSTRIDE];
+    __shared__ __attribute__((aligned(16))) float ks0[KLDS ? 4 * KIMG : 1];
+    __shared__ __attribute__((aligned(16))) float ks1[KLDS ? 4 * KIMG : 1];
+    float* const mlds = KLDS ? ks0 : lds;      // the waves' merge area
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1285,7 +1311,82 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
             }
     };
 
-    if constexpr (DBUF) {
+    if constexpr (KLDS) {
+        // Every load of the loop is a buffer load issued by all lanes (no
+        // branches around loads), so the wave's vmcnt counts are exact and
+        // the waits below name exactly the block they need.
+        // Per-lane DMA offsets, the same for every block: image position
+        // 64 i + lane is chunk pos % KCH of row pos / KCH (pad chunks and
+        // columns past d fetch column 0); lanes past the image fetch out of
+        // range (zeros) into the slot's slack after the image.
+        int kvoff[KRUNS];
+#pragma unroll
+        for (int i = 0; i < KRUNS; ++i) {
+            const int pos = 64 * i + lane;
+            const int r = pos / KCH, ci = pos % KCH;
+            const int col = (ci < D / 4 && 4 * ci < d) ? 4 * ci : 0;
+            kvoff[i] = pos < KTOT ? 4 * (r * d + col) : 0x40000000;
+        }
+        // V (A operand of O^T): rows 4lg + r, columns 64hh + 4lr; columns
+        // past d read out of range, as zeros (their O columns are not stored).
+        int vvoff[4 * NVL];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int hh = 0; hh < NVL; ++hh)
+                vvoff[r * NVL + hh] = 64 * hh + 4 * lr < d ? 4 * ((4 * lg + r) * d + 64 * hh + 4 * lr) : 0x40000000;
+        // Block kb: K into a slot, V into registers.  The buffer ranges end at
+        // kend, so rows past it read as zeros (masked to -inf in finish).
+        auto load_block = [&](int kb, float* slot, R* vv) {
+            const int bytes = min(16, kend - kb) * d * 4;
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(reinterpret_cast<const float*>(Kh) + (size_t)kb * d), (short)0, bytes, 0x00020000);
+            const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(reinterpret_cast<const float*>(Vh) + (size_t)kb * d), (short)0, bytes, 0x00020000);
+            float* dst = slot + wave * KIMG;
+#pragma unroll
+            for (int i = 0; i < KRUNS; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + 256 * i),
+                                                         16, kvoff[i], 0, 0, FA_DECODE_KLDS_AUX);
+#pragma unroll
+            for (int j = 0; j < 4 * NVL; ++j)
+                vv[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, vvoff[j], 0, 2));
+        };
+        auto read_k = [&](const float* slot, R* kk) {
+#pragma unroll
+            for (int cc = 0; cc < NKL; ++cc)
+                kk[cc] = *reinterpret_cast<const f32x4*>(slot + wave * KIMG + lr * KLD + 4 * (4 * cc + lg));
+        };
+        // DMA issued after a block's slot: its KRUNS runs and the 4 * NVL V loads
+        constexpr int AFTER = KRUNS + 4 * NVL;
+        R kk[NKL], va[4 * NVL], vb2[4 * NVL];
+        int kb = kbeg;
+        wait_vmcnt<0>();   // Q resident: the loop's waits then only concern blocks
+        if (kb < kend) load_block(kb, ks0, va);
+        while (kb < kend) {
+            bool nx = kb + kstep < kend;
+            if (nx) {
+                load_block(kb + kstep, ks1, vb2);
+                wait_vmcnt<AFTER>();
+            } else {
+                wait_vmcnt<0>();
+            }
+            read_k(ks0, kk);
+            finish(kb, scores(kb, kk), va);
+            kb += kstep;
+            if (kb >= kend) break;
+            nx = kb + kstep < kend;
+            if (nx) {
+                load_block(kb + kstep, ks0, va);
+                wait_vmcnt<AFTER>();
+            } else {
+                wait_vmcnt<0>();
+            }
+            read_k(ks1, kk);
+            finish(kb, scores(kb, kk), vb2);
+            kb += kstep;
+        }
+    } else if constexpr (DBUF) {
         R ka[NKL], va[4 * NVL], kb2[NKL], vb2[4 * NVL];
         int kb = kbeg;
         if (kb < kend) {
@@ -1324,9 +1425,11 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
 
     l = row4_sum(l);
 
-    // Merge the 4 waves through LDS: waves 1..3 write, wave 0 combines.
+    // Merge the 4 waves through LDS: waves 1..3 write, wave 0 combines (with
+    // LDS-staged K, into slot 0 once every wave has read its last block).
+    if constexpr (KLDS) __syncthreads();
     if (wave != 0) {
-        float* w = lds + (wave - 1) * WSTRIDE;
+        float* w = mlds + (wave - 1) * WSTRIDE;
 #pragma unroll
         for (int j = 0; j < NOB; ++j)
 #pragma unroll
@@ -1340,7 +1443,7 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
     float mn = m;
 #pragma unroll
     for (int w = 0; w < 3; ++w) {
-        mw[w] = lds[w * WSTRIDE + NOB * 4 * 64 + lane];
+        mw[w] = mlds[w * WSTRIDE + NOB * 4 * 64 + lane];
         mn = fmaxf(mn, mw[w]);
     }
     const float mu = (mn == FA_NEG_INF) ? 0.0f : mn;
@@ -1351,11 +1454,11 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
 #pragma unroll
     for (int w = 0; w < 3; ++w) {
         const float cw = rescale_factor(mw[w], mu, c);
-        l += lds[w * WSTRIDE + NOB * 4 * 64 + 64 + lane] * cw;
+        l += mlds[w * WSTRIDE + NOB * 4 * 64 + 64 + lane] * cw;
 #pragma unroll
         for (int j = 0; j < NOB; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) o[j][r] += lds[w * WSTRIDE + (j * 4 + r) * 64 + lane] * cw;
+            for (int r = 0; r < 4; ++r) o[j][r] += mlds[w * WSTRIDE + (j * 4 + r) * 64 + lane] * cw;
     }
     // Partial for (bh, qt, split): O rows (unnormalised), m and l per query.
     const size_t pidx = ((size_t)bh * p.nqt + qt) * p.num_splits + split;
@@ -1714,6 +1817,13 @@ FA_DECODE(128, 1, 3, 2)
 FA_DECODE(128, 0, 3, 2)
 FA_DECODE(256, 1, 1, 1)
 FA_DECODE(256, 0, 1, 1)
+// fa_decode_d{D}_2: K staged through per-wave LDS rings by DMA (f32, D = 64, 128)
+#define FA_DECODE_KLDS(D)                                                                         \
+    extern "C" __global__ void __launch_bounds__(256, 2) fa_decode_d##D##_2(FaParams p) {         \
+        decode_body<D, true, true, float, true>(p);                                               \
+    }
+FA_DECODE_KLDS(64)
+FA_DECODE_KLDS(128)
 
 // fa_decode_{bf16,f16}_d{D}_{VEC}: 16-bit Q/K/V widened to f32 as loaded.
 #define FA_DECODE_LP(D, TN, T, VEC, OCC1, OCC2)                                                   \

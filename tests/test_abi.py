@@ -207,7 +207,7 @@ def test_planning_split_kv():
     assert describe(2, 1, 8, 5, 9000, 256, False).startswith("fa_decode_d256_1")   # 5 rows: 16-row tiles
     assert describe(2, 1, 8, 1, 9000, 18, False).startswith("fa_decode_d32_0")     # d % 4 != 0: tiles
     s = describe(2, 1, 32, 1, 32768, 128, False, fa.PATH_SPLITKV)                  # forced 16-row tiles
-    assert s.startswith("fa_decode_d128_1 grid=16x1x32") and "splits=16 split_len=2048" in s
+    assert s.startswith("fa_decode_d128_2 grid=16x1x32") and "splits=16 split_len=2048" in s
     assert describe(2, 1, 4, 3, 100, 64, False, fa.PATH_SPLITKV_ROWS, 2).startswith("fa_decode_rows_d64_q4 grid=2x1x4")
     for bad in ((2, 1, 4, 5, 1000, 64), (2, 1, 4, 1, 1000, 18)):   # seq_q > 4; d % 4 != 0
         with pytest.raises(fa.FaError) as e:
@@ -225,11 +225,11 @@ def test_planning_split_kv():
     assert "fa_decode" not in describe(2, 1, 32, 16, 200, 128, False)     # short keys: prefill
     assert "fa_decode" not in describe(2, 1, 32, 16, 32768, 128, False, fa.PATH_PREFILL)
     s = describe(2, 1, 1, 40, 300, 64, True, fa.PATH_SPLITKV, 3)
-    assert s.startswith("fa_decode_d64_1 grid=3x3x1") and "splits=3 split_len=128" in s
+    assert s.startswith("fa_decode_d64_2 grid=3x3x1") and "splits=3 split_len=128" in s
     # small f32 prefills (grid below the CU count, <= 128 tiles x heads, >= 256 keys): 16-row tiles
     s = describe(2, 1, 1, 256, 256, 64, False)   # config 1
-    assert s.startswith("fa_decode_d64_1 grid=4x16x1") and "splits=4 split_len=64" in s
-    assert describe(3, 1, 1, 2048, 2048, 128, True).startswith("fa_decode_d128_1 grid=4x128x1")
+    assert s.startswith("fa_decode_d64_2 grid=4x16x1") and "splits=4 split_len=64" in s
+    assert describe(3, 1, 1, 2048, 2048, 128, True).startswith("fa_decode_d128_2 grid=4x128x1")
     assert describe(3, 1, 2, 2048, 2048, 128, True).startswith("fa_prefill_v3_d128_2")   # 256 tiles x heads
     assert describe(3, 1, 1, 200, 200, 64, False).startswith("fa_prefill_v3_d64_2")      # fewer than 256 keys
     assert describe(3, 1, 1, 256, 256, 64, False, dtype=fa.DTYPE_BF16).startswith("fa_prefill_lp_bf16")
