@@ -23,6 +23,7 @@
 #include <cstdlib>
 #include <algorithm>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <thread>
@@ -56,6 +57,20 @@ constexpr size_t kCopySplitMin = size_t(1) << 20;   // smaller copies stay on th
 // per-chunk events cost more than they save on small calls (measured: a
 // 256 x 64 single-head call 78 -> 111 us through the ring).
 constexpr size_t kStageMinBytes = size_t(2) << 20;
+// Host-slice calls in flight at once per device (each with its own stream,
+// device staging buffer and pinned ring; further callers wait for one).
+constexpr int kIoContexts = 4;
+
+// One host-slice call's device-side resources: a stream, a grow-only device
+// staging allocation and a ring of pinned buffers (allocated on first use).
+struct IoContext {
+    hipStream_t stream = nullptr;
+    float* buf = nullptr;
+    size_t floats = 0;
+    char* pin = nullptr;              // kStageBufs x kStageChunk pinned bytes
+    bool pin_tried = false;           // pinned ring unavailable: pageable copies
+    hipEvent_t ev[kStageBufs] = {};   // last DMA on each ring buffer
+};
 
 struct DeviceState {
     std::once_flag once;
@@ -76,15 +91,12 @@ struct DeviceState {
     };
     std::mutex ws_mu;
     std::unordered_map<std::string, Workspace> ws;   // freed by fa_release_stream_workspace
-    // Host-slice calls: one device staging allocation, one pinned ring and
-    // one stream per device.
+    // Host-slice calls: up to kIoContexts contexts, created as concurrent
+    // callers need them and kept; a caller takes a free one for its call.
     std::mutex io_mu;
-    hipStream_t io_stream = nullptr;
-    float* io_buf = nullptr;
-    size_t io_floats = 0;
-    char* io_pin = nullptr;              // kStageBufs x kStageChunk pinned bytes
-    bool io_pin_tried = false;           // pinned ring unavailable: pageable copies
-    hipEvent_t io_ev[kStageBufs] = {};   // last DMA on each ring buffer
+    std::condition_variable io_cv;
+    std::vector<std::unique_ptr<IoContext>> io_all;
+    std::vector<IoContext*> io_free;
 };
 
 // A small pool of host threads for large memcpy's.  One copy at a time
@@ -728,24 +740,24 @@ int check_single(size_t q_len, size_t k_len, size_t v_len, size_t out_len, size_
 
 // The pinned ring of `s` (allocated on first use; false when pinned memory
 // is unavailable, and host slices then take pageable copies).
-bool stage_ring(DeviceState& s) {
-    if (s.io_pin) return true;
-    if (s.io_pin_tried) return false;
-    s.io_pin_tried = true;
+bool stage_ring(IoContext& s) {
+    if (s.pin) return true;
+    if (s.pin_tried) return false;
+    s.pin_tried = true;
     void* pin = nullptr;
     if (hipHostMalloc(&pin, kStageBufs * kStageChunk, hipHostMallocDefault) != hipSuccess) {
         (void)hipGetLastError();
         return false;
     }
     for (int b = 0; b < kStageBufs; ++b) {
-        if (hipEventCreateWithFlags(&s.io_ev[b], hipEventDisableTiming) != hipSuccess) {
+        if (hipEventCreateWithFlags(&s.ev[b], hipEventDisableTiming) != hipSuccess) {
             (void)hipGetLastError();
-            for (int c = 0; c < b; ++c) (void)hipEventDestroy(s.io_ev[c]);
+            for (int c = 0; c < b; ++c) (void)hipEventDestroy(s.ev[c]);
             (void)hipHostFree(pin);
             return false;
         }
     }
-    s.io_pin = static_cast<char*>(pin);
+    s.pin = static_cast<char*>(pin);
     return true;
 }
 
@@ -758,17 +770,17 @@ struct HostSeg {
 // Host -> device through the pinned ring: each chunk is copied into a ring
 // buffer by the copy pool, then queued as a DMA on `st`; a buffer is refilled
 // once its previous DMA has completed.
-int stage_up(DeviceState& s, hipStream_t st, const HostSeg* segs, int nseg) {
+int stage_up(IoContext& s, hipStream_t st, const HostSeg* segs, int nseg) {
     int slot = 0;
     bool used[kStageBufs] = {};
     for (int i = 0; i < nseg; ++i) {
         for (size_t off = 0; off < segs[i].bytes; off += kStageChunk) {
             const size_t len = std::min(kStageChunk, segs[i].bytes - off);
-            char* buf = s.io_pin + slot * kStageChunk;
-            if (used[slot] && hipEventSynchronize(s.io_ev[slot]) != hipSuccess) return FA_ERR_COPY;
+            char* buf = s.pin + slot * kStageChunk;
+            if (used[slot] && hipEventSynchronize(s.ev[slot]) != hipSuccess) return FA_ERR_COPY;
             copy_pool().copy(buf, segs[i].host + off, len);
             if (hipMemcpyAsync(segs[i].dev + off, buf, len, hipMemcpyHostToDevice, st) != hipSuccess ||
-                hipEventRecord(s.io_ev[slot], st) != hipSuccess)
+                hipEventRecord(s.ev[slot], st) != hipSuccess)
                 return FA_ERR_COPY;
             used[slot] = true;
             slot = (slot + 1) % kStageBufs;
@@ -779,30 +791,69 @@ int stage_up(DeviceState& s, hipStream_t st, const HostSeg* segs, int nseg) {
 
 // Device -> host through the pinned ring: up to kStageBufs chunks in flight;
 // each is copied out by the copy pool when its DMA has completed.
-int stage_down(DeviceState& s, hipStream_t st, char* host, const char* dev, size_t bytes) {
+int stage_down(IoContext& s, hipStream_t st, char* host, const char* dev, size_t bytes) {
     const size_t nch = (bytes + kStageChunk - 1) / kStageChunk;
     auto queue = [&](size_t c) {
         const size_t off = c * kStageChunk, len = std::min(kStageChunk, bytes - off);
         const int b = static_cast<int>(c % kStageBufs);
-        return hipMemcpyAsync(s.io_pin + b * kStageChunk, dev + off, len, hipMemcpyDeviceToHost, st) ==
+        return hipMemcpyAsync(s.pin + b * kStageChunk, dev + off, len, hipMemcpyDeviceToHost, st) ==
                        hipSuccess &&
-               hipEventRecord(s.io_ev[b], st) == hipSuccess;
+               hipEventRecord(s.ev[b], st) == hipSuccess;
     };
     for (size_t c = 0; c < nch && c < (size_t)kStageBufs; ++c)
         if (!queue(c)) return FA_ERR_COPY;
     for (size_t c = 0; c < nch; ++c) {
         const int b = static_cast<int>(c % kStageBufs);
         const size_t off = c * kStageChunk, len = std::min(kStageChunk, bytes - off);
-        if (hipEventSynchronize(s.io_ev[b]) != hipSuccess) return FA_ERR_COPY;
-        copy_pool().copy(host + off, s.io_pin + b * kStageChunk, len);
+        if (hipEventSynchronize(s.ev[b]) != hipSuccess) return FA_ERR_COPY;
+        copy_pool().copy(host + off, s.pin + b * kStageChunk, len);
         if (c + kStageBufs < nch && !queue(c + kStageBufs)) return FA_ERR_COPY;
     }
     return FA_OK;
 }
 
+// A free host-slice context of device `dev` for the duration of one call:
+// an idle one, a new one while fewer than kIoContexts exist, or the next one
+// another caller releases.  Its stream is created with the context.
+class IoLease {
+public:
+    explicit IoLease(DeviceState& s) : s_(s) {
+        std::unique_lock<std::mutex> l(s_.io_mu);
+        s_.io_cv.wait(l, [&] { return !s_.io_free.empty() || s_.io_all.size() < (size_t)kIoContexts; });
+        if (!s_.io_free.empty()) {
+            ctx_ = s_.io_free.back();
+            s_.io_free.pop_back();
+            return;
+        }
+        std::unique_ptr<IoContext> c(new (std::nothrow) IoContext());
+        if (!c) return;
+        if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+            (void)hipGetLastError();
+            return;
+        }
+        ctx_ = c.get();
+        s_.io_all.push_back(std::move(c));
+    }
+    ~IoLease() {
+        if (!ctx_) return;
+        {
+            std::lock_guard<std::mutex> l(s_.io_mu);
+            s_.io_free.push_back(ctx_);
+        }
+        s_.io_cv.notify_one();
+    }
+    IoContext* get() const { return ctx_; }
+
+private:
+    DeviceState& s_;
+    IoContext* ctx_ = nullptr;
+};
+
 // Host slices: copy in (Q/K/V elements of `esize` bytes), run
 // `run(stream, dq, dk, dv, dout)` on the device copies, copy the f32 output
-// out, synchronise.  Serialised per device.
+// out, synchronise.  Up to kIoContexts calls per device run at once, each on
+// its own context (the reference's functions are Sync and run concurrently
+// from several threads: src/v2.rs:49-157).
 template <typename F>
 int with_host_slices(const void* q, const void* k, const void* v, size_t esize, size_t bh, size_t sq, size_t sk,
                      size_t d, float* out, F&& run) {
@@ -811,36 +862,30 @@ int with_host_slices(const void* q, const void* k, const void* v, size_t esize, 
     if (rc != FA_OK) return rc;
     rc = ensure_loaded(dev);
     if (rc != FA_OK) return rc;
-    DeviceState& s = g_dev[dev];
-    std::lock_guard<std::mutex> lock(s.io_mu);
-    if (!s.io_stream) {
-        if (hipStreamCreateWithFlags(&s.io_stream, hipStreamNonBlocking) != hipSuccess) {
-            (void)hipGetLastError();
-            s.io_stream = nullptr;
-            return FA_ERR_LAUNCH;
-        }
-    }
+    IoLease lease(g_dev[dev]);
+    if (!lease.get()) return FA_ERR_LAUNCH;
+    IoContext& s = *lease.get();
     // Regions rounded up to 256 bytes keep every operand 256-byte aligned.
     auto up = [](size_t bytes) { return (bytes + 255) / 256 * 256; };
     const size_t nq = bh * sq * d, nk = bh * sk * d;
     const size_t bq = up(nq * esize), bk = up(nk * esize), bo = up(nq * sizeof(float));
     const size_t need = (bq + 2 * bk + bo + sizeof(float) - 1) / sizeof(float);
-    if (need > s.io_floats) {
-        if (s.io_buf) (void)hipFree(s.io_buf);
-        s.io_buf = nullptr;
-        s.io_floats = 0;
-        if (hipMalloc(reinterpret_cast<void**>(&s.io_buf), need * sizeof(float)) != hipSuccess) {
+    if (need > s.floats) {
+        if (s.buf) (void)hipFree(s.buf);
+        s.buf = nullptr;
+        s.floats = 0;
+        if (hipMalloc(reinterpret_cast<void**>(&s.buf), need * sizeof(float)) != hipSuccess) {
             (void)hipGetLastError();
             return FA_ERR_ALLOC;
         }
-        s.io_floats = need;
+        s.floats = need;
     }
-    char* base = reinterpret_cast<char*>(s.io_buf);
+    char* base = reinterpret_cast<char*>(s.buf);
     void* dq = base;
     void* dk = base + bq;
     void* dv = base + bq + bk;
     float* dout = reinterpret_cast<float*>(base + bq + 2 * bk);
-    hipStream_t st = s.io_stream;
+    hipStream_t st = s.stream;
     // On an error, queued DMA may still use the ring: drain the stream first.
     auto fail = [&](int code) {
         (void)hipGetLastError();

@@ -663,6 +663,57 @@ def test_host_slice_calls_from_many_threads():
         assert np.array_equal(out, serial[i]), i
 
 
+def test_host_slice_staged_calls_from_many_threads():
+    """Up to four host-slice calls per device run at once, each with its own
+    stream, device staging buffer and pinned ring (further callers wait for a
+    free one).  Six threads of calls large enough for the pinned ring, f32
+    and bf16 mixed, each repeated: every output equals the device API's on
+    the same inputs, bit for bit."""
+    import threading
+    torch = _torch()
+    dev = torch.device("cuda", 0)
+    shapes = [(8, 2048, 2048, 128, True), (3, 4000, 1500, 100, False), (16, 1000, 1000, 64, True),
+              (1, 3, 300001, 24, False), (6, 1500, 4096, 128, False), (4, 2048, 2048, 128, True)]
+    cases = []
+    for i, (bh, sq, sk, d, causal) in enumerate(shapes):
+        q, k, v = random_vec(bh * sq * d, 90 + i), random_vec(bh * sk * d, 100 + i), random_vec(bh * sk * d, 110 + i)
+        lp = i % 3 == 2 and d % 8 == 0
+        if lp:
+            q16, k16, v16 = (fa.f32_to_bf16_bits(a) for a in (q, k, v))
+            t = [torch.from_numpy(a.view(np.int16)).to(dev) for a in (q16, k16, v16)]
+            out = torch.zeros(bh * sq * d, device=dev)
+            fa.attention_device_lp(fa.DTYPE_BF16, t[0].data_ptr(), t[1].data_ptr(), t[2].data_ptr(), 1, bh, sq, sk,
+                                   d, causal, out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            cases.append((bh, sq, sk, d, causal, (q16, k16, v16), True, out.cpu().numpy()))
+        else:
+            cases.append((bh, sq, sk, d, causal, (q, k, v), False, _device_run(3, q, k, v, bh, sq, sk, d, causal)))
+    errors = []
+
+    def work(i):
+        try:
+            bh, sq, sk, d, causal, (q, k, v), lp, want = cases[i]
+            cfg = fa.FlashAttentionConfig(causal=causal)
+            for rep in range(3):
+                out = np.full(bh * sq * d, 7.0, np.float32)
+                if lp:
+                    fa.flash_attention_multihead_lp(fa.DTYPE_BF16, q, k, v, 1, bh, sq, sk, d, cfg, out)
+                else:
+                    fa.flash_attention_multihead_v3(q, k, v, 1, bh, sq, sk, d, cfg, out)
+                if not np.array_equal(out, want):
+                    errors.append(f"thread {i} call {rep}: differs from the device API")
+        except Exception as e:   # pragma: no cover - reported below
+            errors.append(f"thread {i}: {e!r}")
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(len(cases))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=180)
+    assert not any(t.is_alive() for t in threads), "a thread did not finish"
+    assert not errors, errors
+
+
 def test_host_slices_staged_copies_match_device_api():
     """Host slices move through a ring of 16 MiB pinned buffers, 4 deep; the
     sizes here put segment ends inside chunks, odd byte counts (16-bit inputs),
