@@ -478,8 +478,8 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
                 plan->first.gx = static_cast<unsigned>(s_wgs);
                 std::snprintf(buf, sizeof(buf), "fa_merge_d%d", D);
                 plan->second.name = buf;
-                plan->second.gx = static_cast<unsigned>(bh * sq);   // one wave per output row
-                plan->second.bx = 64;
+                plan->second.gx = static_cast<unsigned>((bh * sq + FA_MERGE_ROWS - 1) / FA_MERGE_ROWS);   // a wave per row
+                plan->second.bx = 64 * FA_MERGE_ROWS;
                 plan->ws_floats = (s_wgs + bh * nqb - 1) * (rows / 16) * (16 * (size_t)D + 32);
                 return FA_OK;
             }
@@ -510,8 +510,8 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
                 plan->first.gx = static_cast<unsigned>(wgs);
                 std::snprintf(buf, sizeof(buf), "fa_merge_d%d", D);
                 plan->second.name = buf;
-                plan->second.gx = static_cast<unsigned>(bh * sq);   // one wave per output row
-                plan->second.bx = 64;
+                plan->second.gx = static_cast<unsigned>((bh * sq + FA_MERGE_ROWS - 1) / FA_MERGE_ROWS);   // a wave per row
+                plan->second.bx = 64 * FA_MERGE_ROWS;
                 plan->ws_floats = bh * nqt * nks * (16 * (size_t)D + 32);
             }
         }
@@ -563,8 +563,8 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     plan->first.bx = 64 * kDecodeWaves;
     std::snprintf(buf, sizeof(buf), "fa_merge_d%d", D);
     plan->second.name = buf;
-    plan->second.gx = static_cast<unsigned>(bh * sq);   // one wave per output row
-    plan->second.bx = 64;
+    plan->second.gx = static_cast<unsigned>((bh * sq + FA_MERGE_ROWS - 1) / FA_MERGE_ROWS);   // a wave per row
+    plan->second.bx = 64 * FA_MERGE_ROWS;
     plan->ws_floats = bh * nqt * nsplit * (16 * (size_t)D + 32);
     return FA_OK;
 }

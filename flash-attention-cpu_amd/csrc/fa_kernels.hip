@@ -1491,11 +1491,24 @@ template <int D>
 __device__ __forceinline__ void merge_body(const FaParams& p) {
     constexpr int CH = D / 4;                // 4-float column chunks per row
     constexpr int GROUPS = 64 / CH > 0 ? 64 / CH : 1;   // lanes sharing a chunk split the splits
-    __shared__ float wts[1024];
-    __shared__ __attribute__((aligned(16))) float part[64 * 4];
+    // FA_MERGE_ROWS rows per workgroup, one wave each with its own LDS area
+    // (waves never wait for each other, so a wave may leave early).
+    __shared__ float wts_all[FA_MERGE_ROWS][1024];
+    __shared__ __attribute__((aligned(16))) float part_all[FA_MERGE_ROWS][64 * 4];
 
-    const int lane = threadIdx.x;
-    const int row = blockIdx.x;              // bh * seq_q + q
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    float* const wts = wts_all[wave];
+    float* const part = part_all[wave];
+    const int row = blockIdx.x * FA_MERGE_ROWS + wave;   // bh * seq_q + q
+    if (row >= p.bh * p.seq_q) return;
+    // orders this wave's LDS writes before its reads of them (a wave's LDS
+    // operations complete in order; this keeps the compiler from moving them)
+    auto wave_sync = [] {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
     const int q = row % p.seq_q, bh = row / p.seq_q;
     const int qt = q / 16, qi = q % 16;
     const float c = p.merge_scale;   // partial maxima -> log2 domain
@@ -1535,7 +1548,7 @@ __device__ __forceinline__ void merge_body(const FaParams& p) {
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off);
-    __syncthreads();
+    wave_sync();
 
     if constexpr (CH > 64) {
         // D > 256: each lane takes chunks lane, lane + 64, ...
@@ -1571,7 +1584,7 @@ __device__ __forceinline__ void merge_body(const FaParams& p) {
     }
     if constexpr (GROUPS > 1) {
         *reinterpret_cast<f32x4*>(part + 4 * lane) = acc;
-        __syncthreads();
+        wave_sync();
         if (grp != 0) return;
         for (int g2 = 1; g2 < GROUPS; ++g2) acc += *reinterpret_cast<const f32x4*>(part + 4 * (g2 * CH + ch));
     }
@@ -1865,7 +1878,7 @@ FA_DECODE_ROWS_LP_ALL(bf16, __bf16)
 FA_DECODE_ROWS_LP_ALL(f16, _Float16)
 
 #define FA_MERGE(D) \
-    extern "C" __global__ void __launch_bounds__(64) fa_merge_d##D(FaParams p) { merge_body<D>(p); }
+    extern "C" __global__ void __launch_bounds__(64 * FA_MERGE_ROWS) fa_merge_d##D(FaParams p) { merge_body<D>(p); }
 FA_MERGE(32)
 FA_MERGE(64)
 FA_MERGE(128)

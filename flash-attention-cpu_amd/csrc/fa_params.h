@@ -59,6 +59,8 @@ typedef struct NaiveParams {
 #ifndef FA_PREFILL_WAVES
 #define FA_PREFILL_WAVES 8
 #endif
+// fa_merge: output rows per workgroup (one wave each).
+#define FA_MERGE_ROWS 4
 #ifdef __cplusplus
 constexpr int fa_prefill_waves(int D) { return D <= 128 ? FA_PREFILL_WAVES : 8; }
 // d_head > 256 (D = 512, 1024): column groups of D / 256 waves share each

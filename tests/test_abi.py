@@ -200,7 +200,7 @@ def test_planning_prefill_kernels():
 def test_planning_split_kv():
     # seq_q <= 4: the row-streaming decode (whole-row K/V loads)
     s = describe(2, 1, 32, 1, 32768, 128, False)
-    assert s.startswith("fa_decode_rows_d128_q1 grid=16x1x32 block=256") and "fa_merge_d128 grid=32x1x1 block=64" in s
+    assert s.startswith("fa_decode_rows_d128_q1 grid=16x1x32 block=256") and "fa_merge_d128 grid=8x1x1 block=256" in s
     assert "splits=16 split_len=2048" in s
     assert describe(3, 1, 32, 2, 32768, 64, False).startswith("fa_decode_rows_d64_q2 grid=16x1x32")
     assert describe(2, 1, 8, 4, 9000, 256, True).startswith("fa_decode_rows_d256_q4")
@@ -241,7 +241,7 @@ def test_planning_stream_split_prefill():
     # 4592 in all -> runs of 18 over 256 workgroups; block slots = 256 + 128 - 1
     # of 8 tiles x (16 x 256 + 32) floats
     s = describe(3, 1, 16, 1000, 1000, 256, True)
-    assert s.startswith("fa_prefill_v3_d256_2s grid=256x1x1 block=512; fa_merge_d256 grid=16000x1x1 block=64; ")
+    assert s.startswith("fa_prefill_v3_d256_2s grid=256x1x1 block=512; fa_merge_d256 grid=4000x1x1 block=256; ")
     assert "stream_per=18" in s and f"workspace={(256 + 128 - 1) * 8 * (16 * 256 + 32) * 4}" in s
     # v2's 32-key stages: 4 + 8 + ... + 28 + 32 = 144 per head -> runs of 9
     assert "grid=256x1x1" in describe(2, 1, 16, 1000, 1000, 256, True) and \
@@ -258,7 +258,7 @@ def test_planning_stream_split_prefill():
 def test_planning_key_split_prefill():
     # config 5c's shape, split forced over 3 workgroups per block
     s = describe(3, 1, 16, 1000, 1000, 256, True, fa.PATH_PREFILL, 3)
-    assert s.startswith("fa_prefill_v3_d256_2 grid=") and "fa_merge_d256 grid=16000x1x1" in s
+    assert s.startswith("fa_prefill_v3_d256_2 grid=") and "fa_merge_d256 grid=4000x1x1" in s
     nks, split_len = int(s.split("splits=")[1].split()[0]), int(s.split("split_len=")[1].split()[0])
     assert split_len % 16 == 0 and nks * split_len >= 1000 > (nks - 1) * split_len
     # compact grid: split y of every 128-row block whose causal key end passes y * split_len
@@ -343,11 +343,11 @@ def test_planning_16bit_inputs():
     assert describe(2, 1, 2, 100, 100, 40, False, dtype=fa.DTYPE_F16).startswith("fa_prefill_lp_f16_d64_2_t1")
     assert describe(2, 1, 2, 100, 100, 20, False, dtype=fa.DTYPE_F16).startswith("fa_prefill_lp_f16_d32_0_t1")
     s = describe(3, 1, 32, 1, 32768, 128, False, dtype=fa.DTYPE_BF16)   # AUTO, seq_q 1: row-streaming decode
-    assert s.startswith("fa_decode_rows_bf16_d128_q1 grid=16x1x32") and "fa_merge_d128 grid=32x1x1" in s
+    assert s.startswith("fa_decode_rows_bf16_d128_q1 grid=16x1x32") and "fa_merge_d128 grid=8x1x1" in s
     s = describe(3, 1, 32, 4, 32768, 128, False, dtype=fa.DTYPE_BF16)   # AUTO, seq_q 4: key-split 16-bit prefill
-    assert s.startswith("fa_prefill_lp_bf16_d128_2") and "fa_merge_d128 grid=128x1x1" in s
+    assert s.startswith("fa_prefill_lp_bf16_d128_2") and "fa_merge_d128 grid=32x1x1" in s
     s = describe(3, 1, 32, 1, 32768, 128, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_BF16)   # split-KV, 16-bit loads
-    assert s.startswith("fa_decode_bf16_d128_1 grid=16x1x32") and "fa_merge_d128 grid=32x1x1" in s
+    assert s.startswith("fa_decode_bf16_d128_1 grid=16x1x32") and "fa_merge_d128 grid=8x1x1" in s
     assert describe(2, 1, 1, 4, 512, 64, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_F16).startswith("fa_decode_f16_d64_1")
     assert describe(3, 1, 1, 4, 512, 62, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_F16).startswith("fa_decode_f16_d64_0")
     with pytest.raises(fa.FaError) as e:
