@@ -291,7 +291,6 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     if (path < FA_PATH_AUTO || path > FA_PATH_STREAM) return FA_ERR_INVALID_ARG;
     if ((path == FA_PATH_SPLITKV || path == FA_PATH_SPLITKV_ROWS || path == FA_PATH_STREAM) && variant == 1)
         return FA_ERR_INVALID_ARG;
-    if (path == FA_PATH_STREAM && lp) return FA_ERR_UNSUPPORTED;   // f32 kernels only
     if (opts && opts->num_splits < 0) return FA_ERR_INVALID_ARG;
     if (d > (size_t)kMaxD) return FA_ERR_UNSUPPORTED;
     // d_head > 256: f32 prefill kernels only (column groups; key split allowed)
@@ -355,11 +354,18 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
         if (nqb * bh > imax) return FA_ERR_UNSUPPORTED;
         p.nqb = static_cast<int>(nqb);
         int lp_tiles = 1;
+        // 16-bit stream split (forced only): the two-tile kernel at D = 128.
+        // AUTO does not take it: measured on config 2 causal bf16 (46.9 ->
+        // 89.9 us) and config 3 (489 -> 568 us), the partials of the split
+        // blocks and their merge cost more than the even runs save at
+        // 16-bit speed.
+        const bool lp_stream = lp && D == 128 && variant != 1 && path == FA_PATH_STREAM;
         if (lp) {
             // Two 16-row tiles per wave halve LDS traffic per row but leave one
             // wave per SIMD in a workgroup running alone: worth it at D = 128
-            // unless the grid is a single round of unequal causal blocks.
-            if (D == 128 && (!causal || nqb * bh > 2 * (size_t)num_cus)) lp_tiles = 2;
+            // unless the grid is a single round of unequal causal blocks (the
+            // stream split evens those out).
+            if (D == 128 && (lp_stream || !causal || nqb * bh > 2 * (size_t)num_cus)) lp_tiles = 2;
             // 0: register-staged scalar loads (any d), 2: global->LDS DMA
             std::snprintf(buf, sizeof(buf), "fa_prefill_lp_%s_d%d_%d_t%d", dtype == FA_DTYPE_BF16 ? "bf16" : "f16",
                           D, vec ? 2 : 0, lp_tiles);
@@ -421,11 +427,12 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
                 return s_segs <= (size_t)kMaxSplits && s_wgs <= imax && s_uhead <= imax && bh * sq <= imax &&
                        s_wgs + bh * nqb <= imax;
             };
+            // workgroups resident at once: the 16-bit kernels fit two per CU at D <= 128
+            const size_t resident = (size_t)num_cus * (lp && D <= 128 ? 2 : 1);
             bool stream = false;
-            if (path == FA_PATH_STREAM) {   // f32 v2/v3 (checked above)
+            if (path == FA_PATH_STREAM) {   // v2/v3 (checked above)
                 if (opts->num_splits > 0 && (size_t)opts->num_splits > imax) return FA_ERR_UNSUPPORTED;
-                if (!stream_fit(opts->num_splits > 0 ? (size_t)opts->num_splits : (size_t)num_cus))
-                    return FA_ERR_UNSUPPORTED;
+                if (!stream_fit(opts->num_splits > 0 ? (size_t)opts->num_splits : resident)) return FA_ERR_UNSUPPORTED;
                 stream = true;
             } else if (opts && opts->num_splits > 1 && path == FA_PATH_PREFILL) {
                 if (opts->num_splits > kMaxSplits) return FA_ERR_UNSUPPORTED;

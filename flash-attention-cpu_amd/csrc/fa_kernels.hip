@@ -1070,15 +1070,13 @@ __device__ __forceinline__ void stream_span(const StreamGeom& g, long long per, 
     last = (ub + stream_stages(g, b) - 1) / per;
 }
 
-// STREAM: the stream-split instantiation (a loop over segments); the others
-// run one segment, so their stage loops keep the registers a loop around
-// them would take (per-lane addresses hoisted out of it stay live).
-template <int D, int VARIANT, int LOADER, bool STREAM>
-__device__ __forceinline__ void prefill_body(const FaParams& p) {
-    constexpr int BQ = fa_prefill_rows(D);
-    constexpr int SK = fa_prefill_stage_keys(D, VARIANT);
+// The segments of this workgroup, run(seg) for each: one (query block, key
+// range) from the grid mapping (key split, two-block pairs when PAIRS and the
+// launch asks for them, or one block), or -- STREAM -- the stream split's
+// run of units, a loop over segments.  BQ rows per block, SK keys per stage.
+template <int BQ, int SK, bool STREAM, bool PAIRS, typename F>
+__device__ __forceinline__ void for_each_segment(const FaParams& p, F&& run) {
     static_assert(BQ % SK == 0, "stream split: whole stages per block");
-    static_assert(!STREAM || VARIANT != 1, "v1 never splits its keys");
     const bool stream = STREAM;
     // Loop state kept in SGPRs (readfirstlane): it is live across every
     // segment's stage loop, where VGPRs are short.  Unit indices fit 32 bits
@@ -1123,16 +1121,28 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
                 seg.slot = y;
                 seg.sbeg = y * (p.split_len / SK);
                 seg.nst = p.split_len / SK;
-            } else if (VARIANT == 3 && D == 128 && p.two_blocks != 0) {
+            } else if (PAIRS && p.two_blocks != 0) {
                 map_pair(p, blockIdx.x, seg.qb, seg.qb_second, seg.bh);
             } else {
                 map_block(p, blockIdx.x, seg.qb, seg.bh);
             }
         }
-        // (the opaque tid spills at D >= 512 and is not needed there)
-        prefill_segment<D, VARIANT, LOADER, STREAM, STREAM && D <= 256>(p, seg);
+        run(seg);
         if (stream) __syncthreads();   // LDS stages and slots are reused by the next segment
     }
+}
+
+// STREAM: the stream-split instantiation (a loop over segments); the others
+// run one segment, so their stage loops keep the registers a loop around
+// them would take (per-lane addresses hoisted out of it stay live).
+template <int D, int VARIANT, int LOADER, bool STREAM>
+__device__ __forceinline__ void prefill_body(const FaParams& p) {
+    static_assert(!STREAM || VARIANT != 1, "v1 never splits its keys");
+    for_each_segment<fa_prefill_rows(D), fa_prefill_stage_keys(D, VARIANT), STREAM, VARIANT == 3 && D == 128>(
+        p, [&](const PrefillSeg& seg) {
+            // (the opaque tid spills at D >= 512 and is not needed there)
+            prefill_segment<D, VARIANT, LOADER, STREAM, STREAM && D <= 256>(p, seg);
+        });
 }
 
 // ---------------------------------------------------------------------------

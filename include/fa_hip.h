@@ -165,10 +165,10 @@ int fa_release_stream_workspace(void* stream);
  * 4 == 0 and 16-byte aligned operands, else FA_ERR_UNSUPPORTED),
  * FA_PATH_STREAM (query-block kernel with the stream split: the key stages
  * of every (slice, query block) cut into equal runs, one per workgroup --
- * num_splits workgroups, 0 = one per CU -- with partials merged where a
- * block is shared; v2/v3, f32).  AUTO picks the row-streaming kernel for
- * decode shapes it supports and the stream split or the key split for
- * prefills smaller than the GPU.
+ * num_splits workgroups, 0 = one per resident workgroup slot -- with
+ * partials merged where a block is shared; v2/v3).  AUTO picks the
+ * row-streaming kernel for decode shapes it supports and the stream split
+ * or the key split for f32 prefills smaller than the GPU.
  * num_splits = 0 lets the library choose (at most 1024). */
 #define FA_PATH_AUTO 0
 #define FA_PATH_PREFILL 1

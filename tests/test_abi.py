@@ -250,9 +250,9 @@ def test_planning_stream_split_prefill():
     assert describe(3, 1, 16, 1000, 1000, 256, True, fa.PATH_STREAM, 100).startswith("fa_prefill_v3_d256_2s grid=100x1x1")
     assert "stream_per=46" in describe(3, 1, 16, 1000, 1000, 256, True, fa.PATH_STREAM, 100)
     assert "stream_per=4" in describe(2, 1, 1, 256, 256, 64, False, fa.PATH_STREAM)   # 4 stages: one run
-    with pytest.raises(fa.FaError) as e:
-        describe(2, 1, 1, 256, 256, 64, False, fa.PATH_STREAM, dtype=fa.DTYPE_BF16)
-    assert e.value.status == fa.FA_ERR_UNSUPPORTED
+    # 16-bit: two resident workgroups per CU at D <= 128
+    assert describe(2, 1, 16, 1000, 1000, 64, True, fa.PATH_STREAM, dtype=fa.DTYPE_BF16).startswith(
+        "fa_prefill_lp_bf16_d64_2_t1s grid=")
 
 
 def test_planning_key_split_prefill():
@@ -337,9 +337,14 @@ def test_bf16_conversion_helpers():
 def test_planning_16bit_inputs():
     s = describe(3, 1, 32, 2048, 2048, 128, True, dtype=fa.DTYPE_BF16)
     assert s.startswith("fa_prefill_lp_bf16_d128_2_t1 grid=512x1x1 block=512")   # one round, causal: 1 tile/wave
+    # forced stream split: two resident two-tile workgroups per CU;
+    # 32 heads x (2 + 4 + ... + 32) = 8704 stages of 64 keys -> 512 runs of 17
+    s = describe(3, 1, 32, 2048, 2048, 128, True, fa.PATH_STREAM, dtype=fa.DTYPE_BF16)
+    assert s.startswith("fa_prefill_lp_bf16_d128_2_t2s grid=512x1x1 block=256") and "stream_per=17" in s
     assert describe(3, 1, 32, 2048, 2048, 128, False, dtype=fa.DTYPE_BF16).startswith(
         "fa_prefill_lp_bf16_d128_2_t2 grid=512x1x1 block=256")
-    assert describe(3, 1, 8, 16384, 16384, 128, True, dtype=fa.DTYPE_BF16).startswith("fa_prefill_lp_bf16_d128_2_t2")
+    assert describe(3, 1, 8, 16384, 16384, 128, True, dtype=fa.DTYPE_BF16).startswith("fa_prefill_lp_bf16_d128_2_t2 ")
+    assert describe(3, 1, 16, 4096, 1024, 256, False, dtype=fa.DTYPE_BF16).startswith("fa_prefill_lp_bf16_d256_2_t1 ")
     assert describe(2, 1, 2, 100, 100, 40, False, dtype=fa.DTYPE_F16).startswith("fa_prefill_lp_f16_d64_2_t1")
     assert describe(2, 1, 2, 100, 100, 20, False, dtype=fa.DTYPE_F16).startswith("fa_prefill_lp_f16_d32_0_t1")
     s = describe(3, 1, 32, 1, 32768, 128, False, dtype=fa.DTYPE_BF16)   # AUTO, seq_q 1: row-streaming decode

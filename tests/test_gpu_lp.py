@@ -146,6 +146,29 @@ def test_lp_key_split_and_determinism(dtype):
         assert_lp(a, want, v32, dtype, f"{NAME[dtype]} auto {bh}x{sq}x{sk} d={d}")
 
 
+@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16])
+def test_lp_stream_split(dtype):
+    """The stream split on the 16-bit kernels (FA_PATH_STREAM; AUTO does not
+    choose it for 16-bit inputs): several workgroup counts at every head
+    width, the two-tile kernel at d_head 65..128, and repeatable results."""
+    rng = np.random.default_rng(13)
+    for bh, sq, sk, d, causal in [(3, 1000, 1000, 128, True), (2, 300, 2000, 128, False), (3, 129, 1025, 64, True),
+                                  (1, 700, 700, 256, True), (5, 77, 300, 32, True), (4, 600, 600, 100, True)]:
+        q16, q32 = to16(rng.standard_normal(bh * sq * d, dtype=np.float32), dtype)
+        k16, k32 = to16(rng.standard_normal(bh * sk * d, dtype=np.float32), dtype)
+        v16, v32 = to16(rng.standard_normal(bh * sk * d, dtype=np.float32), dtype)
+        want = oracle.run(2, q32, k32, v32, bh, sq, sk, d, causal, 64, 128)
+        for splits in (0, 3, 17, 200):
+            plan = fa.describe_launch(3, 1, bh, sq, sk, d, causal, fa.PATH_STREAM, splits, dtype=dtype)
+            assert "stream_per=" in plan, plan
+            got = lp_device(dtype, q16, k16, v16, bh, sq, sk, d, causal, fa.PATH_STREAM, splits)
+            assert_lp(got, want, v32, dtype, f"{NAME[dtype]} stream {splits}: {plan}")
+        if 64 < d <= 128:
+            assert "_t2s " in fa.describe_launch(3, 1, bh, sq, sk, d, causal, fa.PATH_STREAM, dtype=dtype)
+        a = lp_device(dtype, q16, k16, v16, bh, sq, sk, d, causal, fa.PATH_STREAM, 0)
+        assert np.array_equal(a, lp_device(dtype, q16, k16, v16, bh, sq, sk, d, causal, fa.PATH_STREAM, 0))
+
+
 def test_lp_host_slices_shape_errors_and_zero_dims():
     dtype = fa.DTYPE_BF16
     rng = np.random.default_rng(2)
