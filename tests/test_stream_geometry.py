@@ -79,7 +79,17 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("case", CASES)
+def _random_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        bq, skk = [(128, 64), (128, 32), (128, 16), (64, 16), (32, 16)][rng.integers(0, 5)]
+        out.append((int(rng.integers(1, 9)), int(rng.integers(1, 3000)), int(rng.integers(1, 3000)), bq, skk,
+                    bool(rng.integers(0, 2)), int(rng.integers(1, 600))))
+    return out
+
+
+@pytest.mark.parametrize("case", CASES + _random_cases(60, 2024))
 def test_stream_split_covers_every_unit_once(case):
     bh, sq, sk, bq, skk, causal, want = case
     g, nqb, u_head, per, wgs, segs, slots = plan(bh, sq, sk, bq, skk, causal, want)
