@@ -287,6 +287,46 @@ def test_differential_fuzz_split_paths():
             assert np.all(np.abs(out - want) < tol), tag
 
 
+def test_differential_fuzz_new_paths():
+    """Random shapes through the column-group kernels (d_head 257..1024), the
+    stream split (forced, random workgroup counts) and the LDS-staged split-KV
+    tiles (d_head 64 / 128), v2 and v3 against the oracle's CPU v2, with the
+    fuzzer's magnitudes for the split paths (fuzz/fuzz_targets/flash_attention.rs:89-126)
+    and the parity bar for unit-scale inputs."""
+    rng = np.random.default_rng(5150)
+    for it in range(30):
+        kind = it % 3
+        bh = int(rng.integers(1, 4))
+        causal = bool(rng.integers(0, 2))
+        if kind == 0:      # wide heads
+            d = int(rng.integers(257, 1025))
+            sq, sk = int(rng.integers(1, 300)), int(rng.integers(1, 400))
+            path, splits, mag = fa.PATH_AUTO, 0, 1.0
+        elif kind == 1:    # stream split
+            d = int(rng.choice([8, 33, 64, 100, 128, 200, 256, 300, 512]))
+            sq, sk = int(rng.integers(1, 700)), int(rng.integers(1, 900))
+            path, splits, mag = fa.PATH_STREAM, int(rng.integers(0, 300)), float(10.0 ** rng.integers(0, 4))
+        else:              # LDS-staged decode tiles
+            d = int(rng.choice([64, 128, 68, 96, 124]))
+            sq, sk = int(rng.integers(5, 64)), int(rng.integers(300, 5000))
+            path, splits, mag = fa.PATH_SPLITKV, int(rng.integers(0, 40)), float(10.0 ** rng.integers(0, 4))
+        q = (rng.uniform(-1, 1, bh * sq * d) * mag).astype(np.float32)
+        k = (rng.uniform(-1, 1, bh * sk * d) * mag).astype(np.float32)
+        v = (rng.uniform(-1, 1, bh * sk * d)).astype(np.float32)
+        want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+        for variant in (2, 3):
+            plan = fa.describe_launch(variant, 1, bh, sq, sk, d, causal, path, splits)
+            tag = f"it={it} v{variant} ({bh},{sq},{sk},{d},{causal}) mag={mag}: {plan}"
+            print("[case]", tag, flush=True)
+            out = _device_run(variant, q, k, v, bh, sq, sk, d, causal, path, splits, guard=64)
+            if mag == 1.0:
+                assert_parity(out, want, tag)
+            else:
+                assert np.array_equal(np.isfinite(out), np.isfinite(want)), tag
+                tol = 1e-1 * (np.maximum(np.abs(out), np.abs(want)) + 1.0)
+                assert np.all(np.abs(out - want) < tol), tag
+
+
 # ---------------------------------------------------------------------------
 # BASELINE.json configs
 # ---------------------------------------------------------------------------
