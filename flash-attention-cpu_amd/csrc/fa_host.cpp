@@ -384,7 +384,8 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
         plan->ws_floats = 0;
         // Key split for v2/v3 when the grid would leave CUs idle: a query
         // block's keys are cut into splits of `per` stages, one workgroup
-        // each, whose partials fa_merge combines.  Causal blocks differ in
+        // each (the split instantiation, name suffix "s"), whose partials
+        // fa_merge combines.  Causal blocks differ in
         // length, so `per` is chosen to minimise the estimated makespan in
         // key-steps: rounds of resident workgroups (one per CU) x (keys per
         // split + kOverheadKeys for loading Q and writing the partial), plus
@@ -504,6 +505,7 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
             if (per > 0) {
                 const size_t nks = (max_st + per - 1) / per;
                 if (nks > 65535 || nks > (size_t)kMaxSplits) return FA_ERR_UNSUPPORTED;
+                plan->first.name += "s";   // the split instantiation
                 plan->split = true;
                 p.nqt = static_cast<int>(nqt);
                 p.num_splits = static_cast<int>(nks);

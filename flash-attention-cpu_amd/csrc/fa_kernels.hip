@@ -345,8 +345,9 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
     const int g = lane >> 4;                  // lane group 0..3
     const int li = lane & 15;
 
-    // key split: the launch has partials; stream split: this segment's block is shared
-    const bool splitk = STREAM ? seg.slot >= 0 : p.part_o != nullptr;
+    // Split kernels (STREAM): this segment writes a partial -- a piece of a
+    // stream-split block shared with other workgroups, or a key split
+    const bool splitk = STREAM && seg.slot >= 0;
     // two_blocks (v3, no key split): this workgroup runs query blocks
     // nqb-1-r and then r of one (batch, head) -- equal causal work per
     // workgroup, and the second block's loads overlap the first's last step.
@@ -995,8 +996,8 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
         const float lt = row4_sum(l);
         // key split: slot (bh, qt, split); stream split: the block slot
         // (workgroup + global block index) times the block's 16-row tiles
-        const size_t pidx = STREAM ? (size_t)ysplit * TILES + tile
-                                   : ((size_t)bh * p.nqt + qt) * p.num_splits + ysplit;
+        const size_t pidx = p.stream_per > 0 ? (size_t)ysplit * TILES + tile
+                                             : ((size_t)bh * p.nqt + qt) * p.num_splits + ysplit;
         float* po = p.part_o + pidx * 16 * D;
         float* pml = p.part_ml + pidx * 32;
         if (g == 0 && cgrp == 0) {   // (m, l) agree across the column group
@@ -1070,14 +1071,15 @@ __device__ __forceinline__ void stream_span(const StreamGeom& g, long long per, 
     last = (ub + stream_stages(g, b) - 1) / per;
 }
 
-// The segments of this workgroup, run(seg) for each: one (query block, key
-// range) from the grid mapping (key split, two-block pairs when PAIRS and the
-// launch asks for them, or one block), or -- STREAM -- the stream split's
-// run of units, a loop over segments.  BQ rows per block, SK keys per stage.
+// The segments of this workgroup, run(seg) for each.  Split kernels
+// (STREAM): the stream split's run of units (p.stream_per > 0), a loop over
+// segments, or the key split's (block, split) from the compact grid.
+// Otherwise one query block, or two-block pairs when PAIRS and the launch
+// asks for them.  BQ rows per block, SK keys per stage.
 template <int BQ, int SK, bool STREAM, bool PAIRS, typename F>
 __device__ __forceinline__ void for_each_segment(const FaParams& p, F&& run) {
     static_assert(BQ % SK == 0, "stream split: whole stages per block");
-    const bool stream = STREAM;
+    const bool stream = STREAM && p.stream_per > 0;
     // Loop state kept in SGPRs (readfirstlane): it is live across every
     // segment's stage loop, where VGPRs are short.  Unit indices fit 32 bits
     // (the host checks the total).
@@ -1115,7 +1117,7 @@ __device__ __forceinline__ void for_each_segment(const FaParams& p, F&& run) {
             u += (int)cnt;
         } else {
             if (it > 0) break;
-            if (p.part_o != nullptr) {
+            if (STREAM) {   // key split
                 int y;
                 map_block_split(p, seg.qb, seg.bh, y);
                 seg.slot = y;
@@ -1132,9 +1134,10 @@ __device__ __forceinline__ void for_each_segment(const FaParams& p, F&& run) {
     }
 }
 
-// STREAM: the stream-split instantiation (a loop over segments); the others
-// run one segment, so their stage loops keep the registers a loop around
-// them would take (per-lane addresses hoisted out of it stay live).
+// STREAM: the split instantiation (the stream split's loop over segments,
+// or one key-split segment), which writes partials for fa_merge; the others
+// run one unsplit segment, so their stage loops keep the registers that a
+// loop around them, or the partial stores, would take.
 template <int D, int VARIANT, int LOADER, bool STREAM>
 __device__ __forceinline__ void prefill_body(const FaParams& p) {
     static_assert(!STREAM || VARIANT != 1, "v1 never splits its keys");

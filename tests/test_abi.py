@@ -258,7 +258,8 @@ def test_planning_stream_split_prefill():
 def test_planning_key_split_prefill():
     # config 5c's shape, split forced over 3 workgroups per block
     s = describe(3, 1, 16, 1000, 1000, 256, True, fa.PATH_PREFILL, 3)
-    assert s.startswith("fa_prefill_v3_d256_2 grid=") and "fa_merge_d256 grid=4000x1x1" in s
+    assert s.startswith("fa_prefill_v3_d256_2s grid=") and "fa_merge_d256 grid=4000x1x1" in s   # split instantiation
+    assert "stream_per" not in s
     nks, split_len = int(s.split("splits=")[1].split()[0]), int(s.split("split_len=")[1].split()[0])
     assert split_len % 16 == 0 and nks * split_len >= 1000 > (nks - 1) * split_len
     # compact grid: split y of every 128-row block whose causal key end passes y * split_len
@@ -267,7 +268,7 @@ def test_planning_key_split_prefill():
     assert "fa_merge" not in describe(1, 1, 16, 1000, 1000, 256, True)     # v1 never splits
     assert "fa_merge" not in describe(3, 1, 32, 2048, 2048, 128, True)    # full grid
     s = describe(2, 1, 1, 300, 700, 64, False, fa.PATH_PREFILL, 3)   # 11 stages of 64 keys -> 4 per split
-    assert s.startswith("fa_prefill_v2_d64_1 grid=9x1x1") and "splits=3 split_len=256" in s
+    assert s.startswith("fa_prefill_v2_d64_1s grid=9x1x1") and "splits=3 split_len=256" in s
     assert "splits=6 split_len=128" in describe(3, 1, 1, 300, 700, 64, False, fa.PATH_PREFILL, 6)
 
 
@@ -275,19 +276,20 @@ def test_planning_errors():
     # f32 heads of 257..1024 columns: the column-group flash kernels (forced
     # prefill and key splits too); split-KV and 16-bit inputs stop at 256
     assert describe(2, 1, 1, 10, 10, 257, False).startswith("fa_prefill_v2_d512_0 grid=1x1x1 block=512")
-    assert describe(3, 1, 4, 1000, 1000, 512, True).startswith("fa_prefill_v3_d512_2 ")
+    assert describe(3, 1, 4, 1000, 1000, 512, True).startswith("fa_prefill_v3_d512_2s ")   # key split
     assert describe(3, 1, 4, 1000, 1000, 1024, True).startswith("fa_prefill_v3_d1024_1s ")   # one LDS stage
     assert describe(1, 1, 1, 10, 10, 1000, False).startswith("fa_prefill_v1_d1024_1 ")
     assert describe(2, 1, 1, 10, 10, 300, False, fa.PATH_PREFILL).startswith("fa_prefill_v2_d512_1 ")
     s = describe(2, 1, 1, 100, 700, 512, False, fa.PATH_PREFILL, 3)
-    assert s.startswith("fa_prefill_v2_d512_1 ") and "fa_merge_d512" in s and "splits=3" in s
-    assert "fa_merge_d1024" in describe(3, 1, 1, 100, 700, 1024, False, fa.PATH_PREFILL, 3)
+    assert s.startswith("fa_prefill_v2_d512_1s ") and "fa_merge_d512" in s and "splits=3" in s
+    s = describe(3, 1, 1, 100, 700, 1024, False, fa.PATH_PREFILL, 3)
+    assert s.startswith("fa_prefill_v3_d1024_1s ") and "fa_merge_d1024" in s
     for kw in ({"path": fa.PATH_SPLITKV}, {"path": fa.PATH_SPLITKV_ROWS}, {"dtype": fa.DTYPE_BF16}):
         with pytest.raises(fa.FaError) as e:
             describe(2, 1, 1, 10, 10, 257, False, **kw)
         assert e.value.status == fa.FA_ERR_UNSUPPORTED, kw
     # decode shapes at wide heads stay on the prefill kernels
-    assert describe(2, 1, 32, 1, 32768, 512, False).startswith("fa_prefill_v2_d512_1 ")
+    assert describe(2, 1, 32, 1, 32768, 512, False).startswith("fa_prefill_v2_d512_1s ")   # key split
     # wider than 1024: the naive kernels on the automatic path; forced paths
     # and 16-bit inputs are refused
     assert describe(2, 1, 1, 10, 10, 1025, False).startswith("fa_naive_scores_f32")
@@ -350,7 +352,7 @@ def test_planning_16bit_inputs():
     s = describe(3, 1, 32, 1, 32768, 128, False, dtype=fa.DTYPE_BF16)   # AUTO, seq_q 1: row-streaming decode
     assert s.startswith("fa_decode_rows_bf16_d128_q1 grid=16x1x32") and "fa_merge_d128 grid=8x1x1" in s
     s = describe(3, 1, 32, 4, 32768, 128, False, dtype=fa.DTYPE_BF16)   # AUTO, seq_q 4: key-split 16-bit prefill
-    assert s.startswith("fa_prefill_lp_bf16_d128_2") and "fa_merge_d128 grid=32x1x1" in s
+    assert s.startswith("fa_prefill_lp_bf16_d128_2_t2s ") and "fa_merge_d128 grid=32x1x1" in s
     s = describe(3, 1, 32, 1, 32768, 128, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_BF16)   # split-KV, 16-bit loads
     assert s.startswith("fa_decode_bf16_d128_1 grid=16x1x32") and "fa_merge_d128 grid=8x1x1" in s
     assert describe(2, 1, 1, 4, 512, 64, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_F16).startswith("fa_decode_f16_d64_1")

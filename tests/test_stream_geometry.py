@@ -16,6 +16,10 @@ invariants the kernels rely on, against brute-force enumeration:
   (workgroup + global block) are unique and below the slot count the host
   allocates, and the merge's slots for a block are exactly those written;
 * the workgroups sharing one block never exceed the host's slot bound.
+
+The key split's compact grid (map_block_split) is checked the same way: the
+splits whose workgroups store a partial of a block are exactly the splits
+fa_merge reads for its rows.
 """
 from __future__ import annotations
 
@@ -132,3 +136,47 @@ def test_stream_split_covers_every_unit_once(case):
                 assert written[(h, b)] == "direct"
             else:   # fa_merge's slots: first + j + h * nqb + b, j < last - first + 1
                 assert sorted(written[(h, b)]) == [first + j + h * nqb + b for j in range(last - first + 1)]
+
+
+def _key_split_cases():
+    rng = np.random.default_rng(77)
+    cases = [(16, 1000, 1000, 256, True, 3), (1, 300, 700, 64, False, 3), (1, 300, 700, 64, True, 6),
+             (4, 1000, 1000, 512, True, 0), (2, 100, 700, 1024, False, 3), (3, 700, 200, 128, True, 5)]
+    for _ in range(40):
+        cases.append((int(rng.integers(1, 5)), int(rng.integers(1, 1500)), int(rng.integers(1, 3000)),
+                      int(rng.choice([32, 64, 100, 128, 256, 300, 512, 1024])), bool(rng.integers(0, 2)),
+                      int(rng.integers(2, 12))))
+    return cases
+
+
+@pytest.mark.parametrize("case", _key_split_cases())
+def test_key_split_writers_match_merged_splits(case):
+    """map_block_split's compact grid: split y holds every block whose key
+    range reaches y * split_len (causal: blocks qb >= floor(y * split_len /
+    rows)).  For each block, the splits listed (the partials written) must be
+    the splits fa_merge reads: the first min(num_splits, ceil(block key end /
+    split_len))."""
+    import flash_attention_amd as fa
+    bh, sq, sk, d, causal, splits = case
+    try:
+        s = fa.describe_launch(3, 1, bh, sq, sk, d, causal, fa.PATH_PREFILL, splits)
+    except fa.FaError:
+        pytest.skip("plan refused")
+    if "split_len=" not in s or "stream_per" in s:
+        pytest.skip("no key split for this shape")
+    nks = int(s.split("splits=")[1].split()[0])
+    split_len = int(s.split("split_len=")[1].split()[0])
+    grid = int(s.split("grid=")[1].split("x")[0])
+    rows = {512: 64, 1024: 32}.get(max(32, 1 << (d - 1).bit_length()), 128)
+    nqb = -(-sq // rows)
+    writers = [0] * nqb
+    listed = 0
+    for y in range(nks):
+        cnt = nqb - (y * split_len) // rows if causal else nqb
+        for rank in range(max(cnt, 0)):
+            writers[nqb - 1 - rank if causal else rank] += 1
+        listed += max(cnt, 0) * bh
+    assert listed == grid, s
+    for qb in range(nqb):
+        kend = min(sk, (qb + 1) * rows) if causal else sk
+        assert writers[qb] == min(nks, -(-kend // split_len)), (qb, s)
