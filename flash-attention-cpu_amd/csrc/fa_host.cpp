@@ -267,6 +267,8 @@ struct Plan {
 
 // Most splits fa_merge's LDS weight table holds.
 constexpr int kMaxSplits = 1024;
+// Fewest keys per split-KV split the automatic plan makes.
+constexpr size_t kMinSplitKeys = 256;
 
 int pad_d(size_t d) {
     if (d <= 32) return 32;
@@ -324,9 +326,20 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     // with seq_q = 1 and D >= 64.
     const bool rows_ok = !wide && vec && (lp ? (sq == 1 && D >= 64) : sq <= (size_t)kRowsMaxQ);
     if (path == FA_PATH_SPLITKV_ROWS && !rows_ok) return FA_ERR_UNSUPPORTED;
+    // Decode steps (at most two 16-row tiles, 512 keys or more) take
+    // split-KV whatever the grid: a prefill block would hold 1-32 valid
+    // rows of 128 and stream K / V through LDS at under 2 TB/s (measured on
+    // MI355X, d128: 512 slices x 1 query x 1024 keys 285 -> 77 us, 256 x 32
+    // x 2048 283 -> 162 us; at 64 queries and 256 slices the tiles' four K /
+    // V passes cost more, 639 against 558 us).  16-bit inputs: the row
+    // kernel only (sq = 1: 44.1 -> 42.1 us; 16 rows stay on the 16-bit
+    // prefill, 45.9 against 104.7 us).
+    const bool step_shape = sq <= 2 * (size_t)kDecodeRows && sk >= 512 && (!lp || rows_ok);
     bool split = false;
     if (variant != 1) {
         if (path == FA_PATH_SPLITKV || path == FA_PATH_SPLITKV_ROWS) {
+            split = true;
+        } else if (path == FA_PATH_AUTO && !wide && step_shape) {
             split = true;
         } else if (path == FA_PATH_AUTO && nqb * bh < (size_t)num_cus) {
             // Grids smaller than the GPU.  Decode shapes take split-KV.  So do
@@ -533,14 +546,22 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     if (opts && opts->num_splits > 0) {
         nsplit = (size_t)opts->num_splits;
     } else {
-        // resident decode workgroups per CU at the kernel's register use
-        // (D = 256: one, with 424 of 512 registers per lane; the
-        // row-streaming kernel: two)
-        const size_t wg_per_cu = (row_decode || D <= 128) ? 2 : 1;
+        // Workgroups to fill the GPU: the row-streaming kernel and the
+        // 16-row tiles of small prefills two per CU (D = 256 tiles: one,
+        // with 424 of 512 registers per lane); the tiles of decode steps one
+        // per CU with longer splits (measured on MI355X, d128: 64 x 16 x
+        // 4096 4 splits 47.0 us against 8 splits 51.3, config 4b 164.0
+        // against 168.1; while causal 1 x 2048^2 takes 29.0 us in 4 splits
+        // against 31.8 in 2).  At least kMinSplitKeys keys per split:
+        // shorter ones cost more in per-workgroup set-up and merge than they
+        // gain (1 x 1 x 8192: 32 splits 8.2 us, 128 splits 9.2; config 1 in
+        // one split, no merge: 6.4 against 7.4 us).
+        const size_t wg_per_cu = row_decode ? 2 : (D <= 128 && !step_shape ? 2 : 1);
         const size_t slots = wg_per_cu * (size_t)num_cus;
         nsplit = slots / (nqt * bh);
         if (nsplit < 1) nsplit = 1;
         if (nsplit > (size_t)kMaxSplits) nsplit = kMaxSplits;
+        nsplit = std::min(nsplit, std::max<size_t>(1, sk / kMinSplitKeys));
     }
     size_t split_len = (sk + nsplit - 1) / nsplit;
     split_len = ((split_len + 63) / 64) * 64;
@@ -570,6 +591,13 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     plan->first.gy = static_cast<unsigned>(nqt);
     plan->first.gz = static_cast<unsigned>(bh);
     plan->first.bx = 64 * kDecodeWaves;
+    if (nsplit == 1) {
+        // one split: each workgroup sees all keys of its rows and writes
+        // them normalised (no partials, no merge)
+        plan->split = false;
+        plan->ws_floats = 0;
+        return FA_OK;
+    }
     std::snprintf(buf, sizeof(buf), "fa_merge_d%d", D);
     plan->second.name = buf;
     plan->second.gx = static_cast<unsigned>((bh * sq + FA_MERGE_ROWS - 1) / FA_MERGE_ROWS);   // a wave per row

@@ -1473,6 +1473,24 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) o[j][r] += mlds[w * WSTRIDE + (j * 4 + r) * 64 + lane] * cw;
     }
+    if (p.part_o == nullptr) {
+        // One split (no workspace): the workgroup saw every key of its rows,
+        // so it writes them normalised and no merge runs.
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        if (q0 + lr < seq_q) {
+            float* orow = p.out + ((size_t)bh * seq_q + q0 + lr) * d;
+#pragma unroll
+            for (int hh = 0; hh < NVL; ++hh)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int dv0 = 64 * hh + VW * (4 * lg + r);
+#pragma unroll
+                    for (int j = 0; j < VW; ++j)
+                        if (dv0 + j < d) orow[dv0 + j] = o[hh * VW + j][r] * inv;
+                }
+        }
+        return;
+    }
     // Partial for (bh, qt, split): O rows (unnormalised), m and l per query.
     const size_t pidx = ((size_t)bh * p.nqt + qt) * p.num_splits + split;
     float* po = p.part_o + pidx * 16 * D;

@@ -207,7 +207,7 @@ def test_planning_split_kv():
     assert describe(2, 1, 8, 5, 9000, 256, False).startswith("fa_decode_d256_1")   # 5 rows: 16-row tiles
     assert describe(2, 1, 8, 1, 9000, 18, False).startswith("fa_decode_d32_0")     # d % 4 != 0: tiles
     s = describe(2, 1, 32, 1, 32768, 128, False, fa.PATH_SPLITKV)                  # forced 16-row tiles
-    assert s.startswith("fa_decode_d128_2 grid=16x1x32") and "splits=16 split_len=2048" in s
+    assert s.startswith("fa_decode_d128_2 grid=8x1x32") and "splits=8 split_len=4096" in s    # one per CU
     assert describe(2, 1, 4, 3, 100, 64, False, fa.PATH_SPLITKV_ROWS, 2).startswith("fa_decode_rows_d64_q4 grid=2x1x4")
     for bad in ((2, 1, 4, 5, 1000, 64), (2, 1, 4, 1, 1000, 18)):   # seq_q > 4; d % 4 != 0
         with pytest.raises(fa.FaError) as e:
@@ -226,9 +226,21 @@ def test_planning_split_kv():
     assert "fa_decode" not in describe(2, 1, 32, 16, 32768, 128, False, fa.PATH_PREFILL)
     s = describe(2, 1, 1, 40, 300, 64, True, fa.PATH_SPLITKV, 3)
     assert s.startswith("fa_decode_d64_2 grid=3x3x1") and "splits=3 split_len=128" in s
+    # decode steps (<= 32 queries, >= 512 keys) take split-KV whatever the grid; one split
+    # writes its rows directly (no workspace, no merge)
+    assert describe(2, 1, 512, 1, 1024, 128, False) == "fa_decode_rows_d128_q1 grid=1x1x512 block=256"
+    assert describe(2, 1, 256, 1, 4096, 128, False).startswith("fa_decode_rows_d128_q1 grid=2x1x256")
+    assert describe(2, 1, 256, 32, 2048, 128, False) == "fa_decode_d128_2 grid=1x2x256 block=256"
+    assert describe(2, 1, 256, 16, 1024, 256, False) == "fa_decode_d256_1 grid=1x1x256 block=256"
+    assert describe(2, 1, 256, 64, 4096, 128, False).startswith("fa_prefill_v2_d128_1 ")   # 4 tiles: prefill
+    assert describe(3, 1, 512, 1, 1024, 128, False, dtype=fa.DTYPE_BF16).startswith(
+        "fa_decode_rows_bf16_d128_q1 grid=1x1x512")
+    assert describe(3, 1, 256, 16, 2048, 128, False, dtype=fa.DTYPE_BF16).startswith("fa_prefill_lp_bf16")
+    # tiles of decode steps one per CU, at least 256 keys per split
+    assert "splits=4 split_len=1024" in describe(2, 1, 64, 16, 4096, 128, False)
+    assert "splits=32 split_len=256" in describe(2, 1, 1, 1, 8192, 128, False)
     # small f32 prefills (grid below the CU count, <= 128 tiles x heads, >= 256 keys): 16-row tiles
-    s = describe(2, 1, 1, 256, 256, 64, False)   # config 1
-    assert s.startswith("fa_decode_d64_2 grid=4x16x1") and "splits=4 split_len=64" in s
+    assert describe(2, 1, 1, 256, 256, 64, False) == "fa_decode_d64_2 grid=1x16x1 block=256"   # config 1
     assert describe(3, 1, 1, 2048, 2048, 128, True).startswith("fa_decode_d128_2 grid=4x128x1")
     assert describe(3, 1, 2, 2048, 2048, 128, True).startswith("fa_prefill_v3_d128_2")   # 256 tiles x heads
     assert describe(3, 1, 1, 200, 200, 64, False).startswith("fa_prefill_v3_d64_2")      # fewer than 256 keys
@@ -354,7 +366,7 @@ def test_planning_16bit_inputs():
     s = describe(3, 1, 32, 4, 32768, 128, False, dtype=fa.DTYPE_BF16)   # AUTO, seq_q 4: key-split 16-bit prefill
     assert s.startswith("fa_prefill_lp_bf16_d128_2_t2s ") and "fa_merge_d128 grid=32x1x1" in s
     s = describe(3, 1, 32, 1, 32768, 128, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_BF16)   # split-KV, 16-bit loads
-    assert s.startswith("fa_decode_bf16_d128_1 grid=16x1x32") and "fa_merge_d128 grid=8x1x1" in s
+    assert s.startswith("fa_decode_bf16_d128_1 grid=8x1x32") and "fa_merge_d128 grid=8x1x1" in s
     assert describe(2, 1, 1, 4, 512, 64, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_F16).startswith("fa_decode_f16_d64_1")
     assert describe(3, 1, 1, 4, 512, 62, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_F16).startswith("fa_decode_f16_d64_0")
     with pytest.raises(fa.FaError) as e:

@@ -494,6 +494,51 @@ def test_row_streaming_decode_matches_oracle():
         fa.describe_launch(2, 1, 4, 1, 1000, 17, False, fa.PATH_SPLITKV_ROWS)    # d % 4 != 0
 
 
+def test_single_split_decode_writes_rows_directly():
+    """One key split: the decode kernels write the normalised rows themselves -- no workspace,
+    no merge launch -- for the 16-row tiles (every padded width, causal and
+    ragged) and the row-streaming kernel (1-4 rows)."""
+    rng = np.random.default_rng(31)
+    cases = [(fa.PATH_SPLITKV, 2, 16, 700, 64, False), (fa.PATH_SPLITKV, 1, 5, 333, 17, True),
+             (fa.PATH_SPLITKV, 3, 40, 300, 128, True), (fa.PATH_SPLITKV, 1, 20, 257, 256, False),
+             (fa.PATH_SPLITKV, 2, 9, 129, 33, False), (fa.PATH_SPLITKV_ROWS, 4, 1, 900, 128, False),
+             (fa.PATH_SPLITKV_ROWS, 2, 3, 70, 64, True), (fa.PATH_SPLITKV_ROWS, 1, 4, 513, 256, False),
+             (fa.PATH_SPLITKV_ROWS, 3, 2, 64, 32, True)]
+    for path, bh, sq, sk, d, causal in cases:
+        plan = fa.describe_launch(2, 1, bh, sq, sk, d, causal, path, 1)
+        assert "fa_decode" in plan and "fa_merge" not in plan and "workspace" not in plan, plan
+        q = rng.standard_normal(bh * sq * d, dtype=np.float32)
+        k = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        v = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+        for variant in (2, 3):
+            tag = f"v{variant} {plan} ({bh},{sq},{sk},{d},{causal})"
+            print("[case]", tag, flush=True)
+            assert_parity(_device_run(variant, q, k, v, bh, sq, sk, d, causal, path, 1, guard=64), want, tag)
+
+
+def test_batched_decode_steps_take_split_kv():
+    """Decode steps of many slices (a grid of at least one prefill block per
+    CU) run the decode kernels, in one split when the slices alone fill the
+    GPU: the row kernel (1-4 queries) and the 16-row tiles (up to 32), v2 and
+    v3 against the oracle, with a guard around the output."""
+    rng = np.random.default_rng(47)
+    for bh, sq, sk, d, causal, kernel in [(512, 1, 1024, 128, False, "fa_decode_rows_d128_q1 grid=1x1x512"),
+                                          (300, 3, 700, 64, True, "fa_decode_rows_d64_q4 grid=1x1x300"),
+                                          (256, 32, 600, 128, False, "fa_decode_d128_2 grid=1x2x256"),
+                                          (260, 20, 530, 40, True, "fa_decode_d64_2 grid=1x2x260")]:
+        plan = fa.describe_launch(2, 1, bh, sq, sk, d, causal)
+        assert plan.startswith(kernel) and "fa_merge" not in plan, plan
+        q = rng.standard_normal(bh * sq * d, dtype=np.float32)
+        k = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        v = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+        for variant in (2, 3):
+            tag = f"v{variant} {plan}"
+            print("[case]", tag, flush=True)
+            assert_parity(_device_run(variant, q, k, v, bh, sq, sk, d, causal, guard=64), want, tag)
+
+
 def test_small_prefill_on_split_kv_tiles_matches_oracle():
     """Grids smaller than the GPU with at most 128 16-row tiles x heads and
     256+ keys run on the split-KV 16-row tiles (AUTO): long query ranges,
