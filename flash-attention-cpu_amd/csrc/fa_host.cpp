@@ -326,15 +326,16 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     // with seq_q = 1 and D >= 64.
     const bool rows_ok = !wide && vec && (lp ? (sq == 1 && D >= 64) : sq <= (size_t)kRowsMaxQ);
     if (path == FA_PATH_SPLITKV_ROWS && !rows_ok) return FA_ERR_UNSUPPORTED;
-    // Decode steps (at most two 16-row tiles, 512 keys or more) take
-    // split-KV whatever the grid: a prefill block would hold 1-32 valid
-    // rows of 128 and stream K / V through LDS at under 2 TB/s (measured on
-    // MI355X, d128: 512 slices x 1 query x 1024 keys 285 -> 77 us, 256 x 32
-    // x 2048 283 -> 162 us; at 64 queries and 256 slices the tiles' four K /
-    // V passes cost more, 639 against 558 us).  16-bit inputs: the row
-    // kernel only (sq = 1: 44.1 -> 42.1 us; 16 rows stay on the 16-bit
-    // prefill, 45.9 against 104.7 us).
-    const bool step_shape = sq <= 2 * (size_t)kDecodeRows && sk >= 512 && (!lp || rows_ok);
+    // Decode steps (at most two 16-row tiles) take split-KV whatever the
+    // grid and the key count: a prefill block would hold 1-32 valid rows of
+    // 128 and stream K / V through LDS at under 2 TB/s (measured on MI355X,
+    // d128: 512 slices x 1 query x 1024 keys 285 -> 77 us, 256 x 32 x 2048
+    // 283 -> 162 us, 512 x 1 x 64 21.2 -> 5.5 us, 256 x 16 x 64 11.4 -> 7.7
+    // us; at 64 queries and 256 slices the tiles' four K / V passes cost
+    // more, 639 against 558 us).  16-bit inputs: the row kernel only (sq =
+    // 1: 14.6 -> 12.7 us at 256 keys, 44.1 -> 42.1 at 1024; 16 rows stay on
+    // the 16-bit prefill, 45.9 against 104.7 us).
+    const bool step_shape = sq <= 2 * (size_t)kDecodeRows && (!lp || rows_ok);
     bool split = false;
     if (variant != 1) {
         if (path == FA_PATH_SPLITKV || path == FA_PATH_SPLITKV_ROWS) {

@@ -222,11 +222,13 @@ def test_planning_split_kv():
     assert e.value.status == fa.FA_ERR_INVALID_ARG
     assert "fa_decode" in describe(3, 1, 32, 16, 32768, 128, False)
     assert "fa_decode" not in describe(1, 1, 32, 16, 32768, 128, False)   # v1 keeps FA-1's loop
-    assert "fa_decode" not in describe(2, 1, 32, 16, 200, 128, False)     # short keys: prefill
+    assert "fa_decode" in describe(2, 1, 32, 16, 200, 128, False)         # short keys too
+    assert describe(2, 1, 512, 1, 64, 128, False) == "fa_decode_rows_d128_q1 grid=1x1x512 block=256"
+    assert "fa_decode" not in describe(2, 1, 32, 33, 200, 128, False)     # three tiles, short keys: prefill
     assert "fa_decode" not in describe(2, 1, 32, 16, 32768, 128, False, fa.PATH_PREFILL)
     s = describe(2, 1, 1, 40, 300, 64, True, fa.PATH_SPLITKV, 3)
     assert s.startswith("fa_decode_d64_2 grid=3x3x1") and "splits=3 split_len=128" in s
-    # decode steps (<= 32 queries, >= 512 keys) take split-KV whatever the grid; one split
+    # decode steps (<= 32 queries) take split-KV whatever the grid; one split
     # writes its rows directly (no workspace, no merge)
     assert describe(2, 1, 512, 1, 1024, 128, False) == "fa_decode_rows_d128_q1 grid=1x1x512 block=256"
     assert describe(2, 1, 256, 1, 4096, 128, False).startswith("fa_decode_rows_d128_q1 grid=2x1x256")
