@@ -32,6 +32,8 @@ STATED = {   # name: (GFLOP, bytes)
     # 4 * d * 2048 * 2049 / 2 * heads; Q, K, V, O of heads x 2048 x d f32
     "wide_d512": (68.753, 268435456),
     "wide_d1024": (68.753, 268435456),
+    # 4 * 128 * 4096 * 512; 4 * 512 * 128 * (2 * 1 + 2 * 4096)
+    "decode_batched": (1.0737, 2148007936),
 }
 
 
