@@ -358,7 +358,8 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
         }
     }
     const bool row_decode = split && rows_ok && (path == FA_PATH_SPLITKV_ROWS || path == FA_PATH_AUTO);
-    if (split && nqt * bh > 65535) {
+    // split-KV grid: splits x tiles x slices workgroups in one dimension
+    if (split && nqt * bh > imax / (size_t)kMaxSplits) {
         if (path == FA_PATH_SPLITKV || path == FA_PATH_SPLITKV_ROWS) return FA_ERR_UNSUPPORTED;
         split = false;
     }
@@ -588,9 +589,7 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
         std::snprintf(buf, sizeof(buf), "fa_decode_d%d_%d", D, vec ? (D == 64 || D == 128 ? 2 : 1) : 0);
     }
     plan->first.name = buf;
-    plan->first.gx = static_cast<unsigned>(nsplit);
-    plan->first.gy = static_cast<unsigned>(nqt);
-    plan->first.gz = static_cast<unsigned>(bh);
+    plan->first.gx = static_cast<unsigned>(nsplit * nqt * bh);   // split-fastest, then tile, then slice
     plan->first.bx = 64 * kDecodeWaves;
     if (nsplit == 1) {
         // one split: each workgroup sees all keys of its rows and writes

@@ -1152,7 +1152,7 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
 // Split-KV decode kernel (new; no counterpart in the reference).
 //
 // For short query blocks against long key ranges.  Workgroup (split, qt, bh)
-// takes keys [split*split_len, +split_len) of one (batch*head) for query rows
+// (linearised split-fastest into blockIdx.x) takes keys [split*split_len, +split_len) of one (batch*head) for query rows
 // 16qt .. 16qt+15 (zero-padded); its 4 waves take consecutive quarters.  A
 // wave streams its keys 16 at a time straight from HBM with 128-bit loads
 // into MFMA operand registers: S^T = K Q^T (K rows as the A operand, Q as B)
@@ -1202,9 +1202,13 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
     const int lg = lane >> 4;          // lane group 0..3
     const int lr = lane & 15;
 
-    const int split = blockIdx.x;
-    const int qt = blockIdx.y;
-    const int bh = blockIdx.z;
+    // Workgroup x = split + num_splits * (qt + nqt * bh): a 1-D grid (any
+    // number of slices), dispatched split-fastest as a 3-D grid would be.
+    const int wgx = blockIdx.x;
+    const int split = wgx % p.num_splits;
+    const int tq = wgx / p.num_splits;
+    const int qt = tq % p.nqt;
+    const int bh = tq / p.nqt;
     const int seq_q = p.seq_q, seq_k = p.seq_k, d = p.d;
     const E* __restrict__ Qh = reinterpret_cast<const E*>(p.q) + (size_t)bh * seq_q * d;
     const E* __restrict__ Kh = reinterpret_cast<const E*>(p.k) + (size_t)bh * seq_k * d;

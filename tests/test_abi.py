@@ -200,15 +200,15 @@ def test_planning_prefill_kernels():
 def test_planning_split_kv():
     # seq_q <= 4: the row-streaming decode (whole-row K/V loads)
     s = describe(2, 1, 32, 1, 32768, 128, False)
-    assert s.startswith("fa_decode_rows_d128_q1 grid=16x1x32 block=256") and "fa_merge_d128 grid=8x1x1 block=256" in s
+    assert s.startswith("fa_decode_rows_d128_q1 grid=512x1x1 block=256") and "fa_merge_d128 grid=8x1x1 block=256" in s
     assert "splits=16 split_len=2048" in s
-    assert describe(3, 1, 32, 2, 32768, 64, False).startswith("fa_decode_rows_d64_q2 grid=16x1x32")
+    assert describe(3, 1, 32, 2, 32768, 64, False).startswith("fa_decode_rows_d64_q2 grid=512x1x1")
     assert describe(2, 1, 8, 4, 9000, 256, True).startswith("fa_decode_rows_d256_q4")
     assert describe(2, 1, 8, 5, 9000, 256, False).startswith("fa_decode_d256_1")   # 5 rows: 16-row tiles
     assert describe(2, 1, 8, 1, 9000, 18, False).startswith("fa_decode_d32_0")     # d % 4 != 0: tiles
     s = describe(2, 1, 32, 1, 32768, 128, False, fa.PATH_SPLITKV)                  # forced 16-row tiles
-    assert s.startswith("fa_decode_d128_2 grid=8x1x32") and "splits=8 split_len=4096" in s    # one per CU
-    assert describe(2, 1, 4, 3, 100, 64, False, fa.PATH_SPLITKV_ROWS, 2).startswith("fa_decode_rows_d64_q4 grid=2x1x4")
+    assert s.startswith("fa_decode_d128_2 grid=256x1x1") and "splits=8 split_len=4096" in s    # one per CU
+    assert describe(2, 1, 4, 3, 100, 64, False, fa.PATH_SPLITKV_ROWS, 2).startswith("fa_decode_rows_d64_q4 grid=8x1x1")
     for bad in ((2, 1, 4, 5, 1000, 64), (2, 1, 4, 1, 1000, 18)):   # seq_q > 4; d % 4 != 0
         with pytest.raises(fa.FaError) as e:
             describe(*bad, False, fa.PATH_SPLITKV_ROWS)
@@ -223,27 +223,30 @@ def test_planning_split_kv():
     assert "fa_decode" in describe(3, 1, 32, 16, 32768, 128, False)
     assert "fa_decode" not in describe(1, 1, 32, 16, 32768, 128, False)   # v1 keeps FA-1's loop
     assert "fa_decode" in describe(2, 1, 32, 16, 200, 128, False)         # short keys too
-    assert describe(2, 1, 512, 1, 64, 128, False) == "fa_decode_rows_d128_q1 grid=1x1x512 block=256"
+    assert describe(2, 1, 512, 1, 64, 128, False) == "fa_decode_rows_d128_q1 grid=512x1x1 block=256"
     assert "fa_decode" not in describe(2, 1, 32, 33, 200, 128, False)     # three tiles, short keys: prefill
     assert "fa_decode" not in describe(2, 1, 32, 16, 32768, 128, False, fa.PATH_PREFILL)
     s = describe(2, 1, 1, 40, 300, 64, True, fa.PATH_SPLITKV, 3)
-    assert s.startswith("fa_decode_d64_2 grid=3x3x1") and "splits=3 split_len=128" in s
+    assert s.startswith("fa_decode_d64_2 grid=9x1x1") and "splits=3 split_len=128" in s
     # decode steps (<= 32 queries) take split-KV whatever the grid; one split
     # writes its rows directly (no workspace, no merge)
-    assert describe(2, 1, 512, 1, 1024, 128, False) == "fa_decode_rows_d128_q1 grid=1x1x512 block=256"
-    assert describe(2, 1, 256, 1, 4096, 128, False).startswith("fa_decode_rows_d128_q1 grid=2x1x256")
-    assert describe(2, 1, 256, 32, 2048, 128, False) == "fa_decode_d128_2 grid=1x2x256 block=256"
-    assert describe(2, 1, 256, 16, 1024, 256, False) == "fa_decode_d256_1 grid=1x1x256 block=256"
+    assert describe(2, 1, 512, 1, 1024, 128, False) == "fa_decode_rows_d128_q1 grid=512x1x1 block=256"
+    # the split-KV grid is one-dimensional: any number of slices (up to 2^31 workgroups)
+    assert describe(2, 1, 70000, 1, 64, 32, False) == "fa_decode_rows_d32_q1 grid=70000x1x1 block=256"
+    assert describe(2, 1, 70000, 20, 300, 64, False) == "fa_decode_d64_2 grid=140000x1x1 block=256"
+    assert describe(2, 1, 256, 1, 4096, 128, False).startswith("fa_decode_rows_d128_q1 grid=512x1x1")
+    assert describe(2, 1, 256, 32, 2048, 128, False) == "fa_decode_d128_2 grid=512x1x1 block=256"
+    assert describe(2, 1, 256, 16, 1024, 256, False) == "fa_decode_d256_1 grid=256x1x1 block=256"
     assert describe(2, 1, 256, 64, 4096, 128, False).startswith("fa_prefill_v2_d128_1 ")   # 4 tiles: prefill
     assert describe(3, 1, 512, 1, 1024, 128, False, dtype=fa.DTYPE_BF16).startswith(
-        "fa_decode_rows_bf16_d128_q1 grid=1x1x512")
+        "fa_decode_rows_bf16_d128_q1 grid=512x1x1")
     assert describe(3, 1, 256, 16, 2048, 128, False, dtype=fa.DTYPE_BF16).startswith("fa_prefill_lp_bf16")
     # tiles of decode steps one per CU, at least 256 keys per split
     assert "splits=4 split_len=1024" in describe(2, 1, 64, 16, 4096, 128, False)
     assert "splits=32 split_len=256" in describe(2, 1, 1, 1, 8192, 128, False)
     # small f32 prefills (grid below the CU count, <= 128 tiles x heads, >= 256 keys): 16-row tiles
-    assert describe(2, 1, 1, 256, 256, 64, False) == "fa_decode_d64_2 grid=1x16x1 block=256"   # config 1
-    assert describe(3, 1, 1, 2048, 2048, 128, True).startswith("fa_decode_d128_2 grid=4x128x1")
+    assert describe(2, 1, 1, 256, 256, 64, False) == "fa_decode_d64_2 grid=16x1x1 block=256"   # config 1
+    assert describe(3, 1, 1, 2048, 2048, 128, True).startswith("fa_decode_d128_2 grid=512x1x1")
     assert describe(3, 1, 2, 2048, 2048, 128, True).startswith("fa_prefill_v3_d128_2")   # 256 tiles x heads
     assert describe(3, 1, 1, 200, 200, 64, False).startswith("fa_prefill_v3_d64_2")      # fewer than 256 keys
     assert describe(3, 1, 1, 256, 256, 64, False, dtype=fa.DTYPE_BF16).startswith("fa_prefill_lp_bf16")
@@ -364,11 +367,11 @@ def test_planning_16bit_inputs():
     assert describe(2, 1, 2, 100, 100, 40, False, dtype=fa.DTYPE_F16).startswith("fa_prefill_lp_f16_d64_2_t1")
     assert describe(2, 1, 2, 100, 100, 20, False, dtype=fa.DTYPE_F16).startswith("fa_prefill_lp_f16_d32_0_t1")
     s = describe(3, 1, 32, 1, 32768, 128, False, dtype=fa.DTYPE_BF16)   # AUTO, seq_q 1: row-streaming decode
-    assert s.startswith("fa_decode_rows_bf16_d128_q1 grid=16x1x32") and "fa_merge_d128 grid=8x1x1" in s
+    assert s.startswith("fa_decode_rows_bf16_d128_q1 grid=512x1x1") and "fa_merge_d128 grid=8x1x1" in s
     s = describe(3, 1, 32, 4, 32768, 128, False, dtype=fa.DTYPE_BF16)   # AUTO, seq_q 4: key-split 16-bit prefill
     assert s.startswith("fa_prefill_lp_bf16_d128_2_t2s ") and "fa_merge_d128 grid=32x1x1" in s
     s = describe(3, 1, 32, 1, 32768, 128, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_BF16)   # split-KV, 16-bit loads
-    assert s.startswith("fa_decode_bf16_d128_1 grid=8x1x32") and "fa_merge_d128 grid=8x1x1" in s
+    assert s.startswith("fa_decode_bf16_d128_1 grid=256x1x1") and "fa_merge_d128 grid=8x1x1" in s
     assert describe(2, 1, 1, 4, 512, 64, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_F16).startswith("fa_decode_f16_d64_1")
     assert describe(3, 1, 1, 4, 512, 62, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_F16).startswith("fa_decode_f16_d64_0")
     with pytest.raises(fa.FaError) as e:

@@ -523,10 +523,12 @@ def test_batched_decode_steps_take_split_kv():
     GPU: the row kernel (1-4 queries) and the 16-row tiles (up to 32), v2 and
     v3 against the oracle, with a guard around the output."""
     rng = np.random.default_rng(47)
-    for bh, sq, sk, d, causal, kernel in [(512, 1, 1024, 128, False, "fa_decode_rows_d128_q1 grid=1x1x512"),
-                                          (300, 3, 700, 64, True, "fa_decode_rows_d64_q4 grid=1x1x300"),
-                                          (256, 32, 600, 128, False, "fa_decode_d128_2 grid=1x2x256"),
-                                          (260, 20, 530, 40, True, "fa_decode_d64_2 grid=1x2x260")]:
+    for bh, sq, sk, d, causal, kernel in [(512, 1, 1024, 128, False, "fa_decode_rows_d128_q1 grid=512x1x1"),
+                                          (300, 3, 700, 64, True, "fa_decode_rows_d64_q4 grid=300x1x1"),
+                                          (256, 32, 600, 128, False, "fa_decode_d128_2 grid=512x1x1"),
+                                          (260, 20, 530, 40, True, "fa_decode_d64_2 grid=520x1x1"),
+                                          # more slices than a 3-D grid's y / z dimension holds
+                                          (70000, 1, 64, 32, False, "fa_decode_rows_d32_q1 grid=70000x1x1")]:
         plan = fa.describe_launch(2, 1, bh, sq, sk, d, causal)
         assert plan.startswith(kernel) and "fa_merge" not in plan, plan
         q = rng.standard_normal(bh * sq * d, dtype=np.float32)
