@@ -12,7 +12,7 @@ while the kernel sources match the ones profiled).
 
 Every other configuration (1, 3, 4a, 4b, 5, 5c; v1/v2/v3), and three shapes
 beyond BASELINE.json (wide heads of d_head 512 and 1024, and a batched decode
-step of 512 slices), is timed the same way into
+step of 768 slices), is timed the same way into
 ``extra.configs`` -- TFLOP/s and % of the FP32-MFMA peak for
 prefill shapes, GB/s and % of 8 TB/s for decode shapes -- next to a CPU
 baseline on the same inputs: the oracle's v2 (oracle/, a C restatement of the
@@ -58,9 +58,11 @@ CONFIGS = [
     # flash kernels (the crate's flash path takes any d_head)
     ("wide_d512", 16, 2048, 2048, 512, True, 1.0, False, "prefill"),
     ("wide_d1024", 8, 2048, 2048, 1024, True, 1.0, False, "prefill"),
-    # batched decode step: 512 (sequence, head) slices of one query over 4096
-    # keys, the split-KV row kernel whatever the grid size
-    ("decode_batched", 512, 1, 4096, 128, False, 1.0, False, "decode"),
+    # batched decode step: 768 (sequence, head) slices of one query over
+    # 2048 keys, the split-KV row kernel whatever the grid size (launch
+    # sizes of its own for every variant: profiles key kernels by name and
+    # launch size)
+    ("decode_batched", 768, 1, 2048, 128, False, 1.0, False, "decode"),
 ]
 HEADLINE = "config2"
 

@@ -32,8 +32,8 @@ STATED = {   # name: (GFLOP, bytes)
     # 4 * d * 2048 * 2049 / 2 * heads; Q, K, V, O of heads x 2048 x d f32
     "wide_d512": (68.753, 268435456),
     "wide_d1024": (68.753, 268435456),
-    # 4 * 128 * 4096 * 512; 4 * 512 * 128 * (2 * 1 + 2 * 4096)
-    "decode_batched": (1.0737, 2148007936),
+    # 4 * 128 * 2048 * 768; 4 * 768 * 128 * (2 * 1 + 2 * 2048)
+    "decode_batched": (0.80531, 1611399168),
 }
 
 
@@ -69,3 +69,23 @@ def test_traffic_lookup_requires_matching_kernel_sources(tmp_path):
     ent["kernel_source_sha256"] = "0" * 16
     path.write_text(json.dumps({"fa_x@64": ent}))
     assert traffic.lookup(str(path), "fa_x", 64) == (None, "profiled on other kernel sources")
+
+
+def test_bench_rows_have_distinct_launch_keys():
+    """profiles/ key kernel figures by (kernel, launch size): two bench rows
+    whose launches share a key would have their counters averaged.  The one
+    shared key is v1 of configs 4a and 4b, the same kernel over the same 32
+    prefill blocks and the same K / V bytes."""
+    import flash_attention_amd as fa
+    use = {}
+    for (name, bh, sq, sk, d, causal, *_rest) in bench.CONFIGS:
+        plans = [fa.describe_launch(v, 1, bh, sq, sk, d, causal) for v in (1, 2, 3)]
+        if name in ("config2", "config3", "config4a", "config5"):
+            plans += [fa.describe_launch(3, 1, bh, sq, sk, d, causal, dtype=t) for t in (fa.DTYPE_BF16, fa.DTYPE_F16)]
+        for plan in plans:
+            for part in plan.split("; "):
+                if "grid=" in part:
+                    use.setdefault((part.split()[0], bench.grid_threads(part)), set()).add(name)
+    shared = {k: v for k, v in use.items() if len(v) > 1}
+    assert shared == {("fa_prefill_v1_d128_1", 16384): {"config4a", "config4b"}}, shared
+
