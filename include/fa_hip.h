@@ -159,16 +159,19 @@ int fa_release_stream_workspace(void* stream);
  * 1/sqrt(d_head).  path: FA_PATH_AUTO (what fa_device_vN does),
  * FA_PATH_PREFILL (query-block kernel; with num_splits > 1 and v2/v3, each
  * block's keys are divided over num_splits workgroups whose partials are
- * merged), FA_PATH_SPLITKV (16-row decode tiles, always split; v2/v3 only),
+ * merged), FA_PATH_SPLITKV (16-row decode tiles; with one split -- num_splits
+ * = 1, or chosen -- each tile is written directly, no merge; v2/v3 only),
  * FA_PATH_SPLITKV_ROWS (row-streaming split-KV for seq_len_q <= 4: K and V
  * read as whole rows, dot products on the vector ALUs; v2/v3, f32, d_head %
  * 4 == 0 and 16-byte aligned operands, else FA_ERR_UNSUPPORTED),
  * FA_PATH_STREAM (query-block kernel with the stream split: the key stages
  * of every (slice, query block) cut into equal runs, one per workgroup --
  * num_splits workgroups, 0 = one per resident workgroup slot -- with
- * partials merged where a block is shared; v2/v3).  AUTO picks the
- * row-streaming kernel for decode shapes it supports and the stream split
- * or the key split for f32 prefills smaller than the GPU.
+ * partials merged where a block is shared; v2/v3).  AUTO (v2/v3) runs
+ * decode steps -- seq_len_q <= 32, any batch and key count -- on split-KV
+ * (the row-streaming kernel where it applies, else 16-row tiles; 16-bit
+ * inputs only on the row kernel), and the stream split or the key split for
+ * prefills smaller than the GPU.
  * num_splits = 0 lets the library choose (at most 1024). */
 #define FA_PATH_AUTO 0
 #define FA_PATH_PREFILL 1
