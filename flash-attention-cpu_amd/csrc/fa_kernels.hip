@@ -65,6 +65,11 @@ constexpr float kLazyMax = 8.0f;
 #ifndef FA_FILL_HALF
 #define FA_FILL_HALF 1
 #endif
+// v3 prefill, D = 128: the non-filling waves take each stage's softmax
+// before the step's barrier, their partners after it.
+#ifndef FA_SPLIT_SOFTMAX
+#define FA_SPLIT_SOFTMAX 1
+#endif
 
 // ---------------------------------------------------------------------------
 // Small device helpers
@@ -831,6 +836,13 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
         // together need more than 256 VGPRs (39 spilled; 274 -> 288 us).
         constexpr bool EARLY_OK = D != 128 && CG == 1;
         const bool early = EARLY_OK && FW < NW && fwave < 0;
+        // D = 128: the same split of the softmax between the two waves of a
+        // SIMD within one loop copy -- the softmax has two call sites in the
+        // step, taken by a wave-uniform flag (the barrier stays put; same
+        // registers as one order).  Measured: config 2 272.1 -> 269.2 us,
+        // config 3 4016 -> 3975 us, 32 x 2048^2 non-causal 513.6 -> 507.3 us.
+        constexpr bool SPLIT_SM = FA_SPLIT_SOFTMAX && D == 128 && CG == 1;
+        const bool sm_late = SPLIT_SM && FW < NW && fwave < 0;
         f32x4 s_cur[KB];
         bool act_cur = ntot > 0 && gstage_active(0);
         if (act_cur) {
@@ -838,7 +850,7 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
             qk_stage(Kb0, s_cur);
             if constexpr (CG > 1) xs_put(s_cur, 0);   // summed and masked after the barrier
             else mask_stage(s_cur, kb_of(0));
-            if (early) softmax_part(s_cur);
+            if (early || sm_late) softmax_part(s_cur);
         }
         wait_vmcnt<0>();
         __syncthreads();   // V(0), K(1) resident; Kb0 free for K(2)
@@ -921,7 +933,7 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
                 if (act_cur) pv_preload(v_cur);
                 if (act_nxt) qk_preload(k_next);
                 if (act_cur) {
-                    softmax_part(s_cur);
+                    if (!sm_late) softmax_part(s_cur);
                     pv_part(s_cur, v_cur, no_hook);
                 }
                 if (switch_now) do_switch();
@@ -929,6 +941,7 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
                     qk_stage(k_next, s_cur);
                     if constexpr (CG > 1) xs_put(s_cur, 1 - P);
                     else mask_stage(s_cur, kb_of(gs + 1));
+                    if (sm_late) softmax_part(s_cur);
                 }
             }
             if (has_next) {
