@@ -394,6 +394,12 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
     for (int j = 0; j < NOB; ++j) o[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
     float m = FA_NEG_INF;   // reference max of the row's log2-domain scores (same in its 4 lanes)
     float l = 0.0f;         // v2/v3: this lane's partial row sum; v1: full row sum
+    // v1: whether the current stage changes the row (some probability above
+    // zero, or a rescale); a stage that does not -- keys past the row's
+    // causal end, which v1 still visits -- skips the un-normalise /
+    // re-normalise round trip, an identity whose two roundings (o * l, then
+    // o * fl(1/l)) would otherwise drift o once per such stage.
+    bool v1_moves = true;
     // -m (0 while m = -inf) as the QK^T chain's initial accumulator: the MFMA
     // then yields S - m directly, with no per-score subtraction.
     f32x4 nref = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -693,8 +699,10 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
         const bool rescale = grow && seen;
         if (VARIANT == 1) {
             const float corr = rescale ? fa_exp2(-delta) : 1.0f;
-            const float l_new = corr * l + row4_sum(ps);
-            const float f = l * corr;
+            const float rs = row4_sum(ps);
+            const float l_new = corr * l + rs;
+            v1_moves = rescale || rs != 0.0f;
+            const float f = v1_moves ? l * corr : 1.0f;
 #pragma unroll
             for (int j = 0; j < NOB; ++j) o[j] *= f;
             l = l_new;
@@ -745,7 +753,7 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
             }
         }
         if (VARIANT == 1) {
-            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            const float inv = !v1_moves ? 1.0f : (l > 0.0f ? 1.0f / l : 0.0f);
 #pragma unroll
             for (int j = 0; j < NOB; ++j) o[j] *= inv;
         }

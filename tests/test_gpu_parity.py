@@ -111,6 +111,29 @@ def test_wide_heads_run_flash_kernels(variant):
     assert max_abs_diff(_device_run(variant, q, k, v, bh, sq, sk, d, True, scale=scale), want2) < 1e-5
 
 
+def test_v1_rows_past_their_causal_end_do_not_drift():
+    """v1 visits every key stage (no causal skip, src/v1.rs:209-216), so a
+    causal row whose visible keys end early meets many stages that add
+    nothing; those skip the un-normalise / re-normalise round trip (an
+    identity whose o * l * fl(1/l) would move o by an ulp-scale step per
+    stage).  Few queries over many keys is the worst case: rows see <= sq keys
+    and then hundreds of empty stages (found by a random differential run:
+    4 x 24 x 5671, d 256, max-abs 2.1e-5 before)."""
+    rng = np.random.default_rng(2024)
+    for bh, sq, sk, d in ((4, 24, 5671, 256), (2, 64, 8192, 128), (1, 40, 3000, 512), (3, 16, 4000, 64)):
+        q = rng.standard_normal(bh * sq * d, dtype=np.float32)
+        k = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        v = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        want = cpu_v2(q, k, v, bh, sq, sk, d, True)
+        tag = f"v1 ({bh},{sq},{sk},{d}) causal: {fa.describe_launch(1, 1, bh, sq, sk, d, True)}"
+        print("[case]", tag, flush=True)
+        got = _device_run(1, q, k, v, bh, sq, sk, d, True, guard=64)
+        assert_parity(got, want, tag)
+        # as close to v2 as v2's own kernel is (no per-stage drift left)
+        v2 = _device_run(2, q, k, v, bh, sq, sk, d, True)
+        assert max_abs_diff(got, want) < 2.0 * max_abs_diff(v2, want) + 2e-6, tag
+
+
 @pytest.mark.parametrize("d", (384, 512, 1024))
 def test_wide_heads_multiblock_and_key_split(d):
     """Several query blocks with causal skipping, ragged ends, and the key
