@@ -216,9 +216,10 @@ int fa_device_ex_noalloc(int variant, void* stream, const float* q, const float*
  * hold bfloat16 (FA_DTYPE_BF16, raw 16-bit patterns) or IEEE binary16
  * (FA_DTYPE_F16) in the layout of the f32 entry points; O is f32.  QK^T and PV
  * run on 16-bit MFMA with f32 accumulation (every product exact), the softmax
- * in f32, and the probabilities are rounded to the input type for PV, so
- * each output element is within u * max|V| of f32 attention on the same
- * 16-bit inputs (u = 2^-8 bf16, 2^-11 f16).  Causal masking, shape checks and
+ * in f32, and the probabilities are rounded to the input type for PV (the
+ * row sums add up the rounded values), so each output element is within
+ * u/(1-u) * max|V| of f32 attention on the same 16-bit inputs (u = 2^-8
+ * bf16, 2^-11 f16).  Causal masking, shape checks and
  * zero-dimension behaviour are those of fa_multihead_v2; d_head <= 256.  The
  * algorithm is v2/v3's (deferred normalisation, causal skip); no variant
  * argument.  opts: softmax_scale, path and num_splits as for fa_device_ex;
