@@ -37,6 +37,9 @@ GUARD = 64
 @pytest.fixture(scope="module", autouse=True)
 def _device():
     fa.init()
+    yield
+    # hand the tens of GB these tests held back to the device for later tests
+    _torch().cuda.empty_cache()
 
 
 def _torch():
