@@ -25,8 +25,12 @@ top-level ``parity`` object.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--variant 3]
                        [--quick | --configs config2,config4a,...]
-                       [--no-cpu-baseline] [--cpu-seconds S]
-Prints exactly one JSON line on stdout; progress goes to stderr.
+                       [--no-cpu-baseline] [--cpu-seconds S] [--csv PATH]
+Prints exactly one JSON line on stdout (compact: per config and variant the
+kernel time, throughput, % of peak, counters where profiled, and parity);
+progress goes to stderr, which ends with a one-line-per-config summary.
+--csv appends one benchmark-history row per config and variant to PATH
+(flash_attention_amd.bench_quick's schema, compared by bench_compare).
 """
 from __future__ import annotations
 
@@ -254,6 +258,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds-other", type=float, default=2.5, help="CPU budget of each other config")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="only run 5 plain device copies of N MiB (rocprofv3 PMC scale reference) and exit")
+    ap.add_argument("--csv", default="", metavar="PATH",
+                    help="append one history row per config and variant to PATH (bench_quick's schema)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -277,24 +283,41 @@ def main() -> int:
         return 0
 
     import flash_attention_amd as fa
-    from flash_attention_amd.traffic import kernel_source_hash, lookup
+    from flash_attention_amd import traffic as trf
 
     fa.init()
     traffic_table = os.path.join(ROOT, "profiles", "traffic.json")
+    pmc_table = os.path.join(ROOT, "profiles", "pmc.json")
     configs = {}
     pending_cpu = []   # (name, workload, host inputs, {variant: GPU output})
     result_head = None
+    history = []       # (name, label, wl, wall ms, kernel ms, entry) for --csv
 
     chosen = {c for c in args.configs.split(",") if c}
     unknown = chosen - {c[0] for c in CONFIGS}
     if unknown:
         print(f"bench.py: unknown config(s) {sorted(unknown)}", file=sys.stderr)
         return 2
+
+    def counters(ent, kernels, ms_kernel):
+        """Measured HBM bytes and PMC figures of the call's first kernel, where profiled on these sources."""
+        key = (kernels.split()[0], grid_threads(kernels))
+        tb, _ = trf.lookup(traffic_table, *key)
+        if tb is not None:
+            ent["hbm_mb"] = round(tb / 1e6, 1)
+        tent = trf.lookup_entry(traffic_table, *key)
+        if tent is not None and ms_kernel > 0:
+            ent["fetch_gbs"] = round(tent["fetch_bytes_per_launch"] / (ms_kernel * 1e-3) / 1e9, 1)
+        pent = trf.lookup_entry(pmc_table, *key)
+        if pent is not None:
+            ent["mfma_busy"] = pent["mfma_busy_pct"]
+            ent["lds_conflicts"] = pent["lds_bank_conflicts"]
+
     for (name, bh, sq, sk, d, causal, sig, vu, kind) in CONFIGS:
         if name != HEADLINE and (args.quick or (chosen and name not in chosen)):
             continue
         wl = Workload(torch, name, bh, sq, sk, d, causal, sig, vu, kind)
-        entry = {"shape": wl.describe(), "algorithmic_flop": wl.flops, "algorithmic_bytes": wl.bytes}
+        entry = {"shape": wl.describe(), "flop": wl.flops, "bytes": wl.bytes}
         outs = {}
         variants = (1, 2, 3)
         if name == HEADLINE:   # the headline variant first, with the requested step counts
@@ -312,28 +335,29 @@ def main() -> int:
                     entry[f"v{var}_median_5x20_us"] = round(reps[2] * 1e3, 1)
             else:
                 steps = auto_steps(torch, call, max(5, args.steps))
-                _, ms_kernel = time_calls(torch, call, steps, 2)
+                ms_step, ms_kernel = time_calls(torch, call, steps, 2)
             torch.cuda.synchronize()
             outs[var] = wl.o.cpu().numpy().copy()
-            ent = {"us_per_call": round(ms_kernel * 1e3, 1), "kernels": kernels}
+            ent = {"us": round(ms_kernel * 1e3, 1)}
             tf = wl.flops / (ms_kernel * 1e-3) / 1e12
-            ent["tflops"] = round(tf, 2)
             if kind == "prefill":
-                ent["pct_fp32_mfma_peak"] = round(100 * tf / PEAK_TFLOPS, 1)
+                ent.update(tflops=round(tf, 2), pct_peak=round(100 * tf / PEAK_TFLOPS, 1))
             else:
                 gbs = wl.bytes / (ms_kernel * 1e-3) / 1e9
-                ent.update(gbs=round(gbs, 1), pct_hbm_peak=round(100 * gbs / PEAK_GBS, 1))
-            tb, why = lookup(traffic_table, kernels.split()[0], grid_threads(kernels))
-            if tb is not None:
-                ent["hbm_bytes_per_launch"] = tb
+                ent.update(gbs=round(gbs, 1), pct_hbm=round(100 * gbs / PEAK_GBS, 1))
+            counters(ent, kernels, ms_kernel)
             entry[f"v{var}"] = ent
-            log(f"[bench] {name} v{var}: {ent}")
+            history.append((name, f"v{var}", wl, ms_step, ms_kernel, ent))
+            log(f"[bench] {name} v{var}: {ent} [{kernels}]")
         if not args.quick and name in ("config2", "config4a"):
             var = args.variant if name == HEADLINE else 2
             ms = time_host_slice(fa, wl, var, 5 if name == "config2" else 2)
-            entry[f"host_slice_v{var}"] = {"ms_per_call": round(ms, 3),
-                                           "tflops_incl_pcie": round(wl.flops / (ms * 1e-3) / 1e12, 3),
-                                           "gbs_incl_pcie": round(wl.bytes / (ms * 1e-3) / 1e9, 1)}
+            hs = {"ms": round(ms, 3)}
+            if kind == "prefill":
+                hs["tflops"] = round(wl.flops / (ms * 1e-3) / 1e12, 2)
+            else:
+                hs["gbs"] = round(wl.bytes / (ms * 1e-3) / 1e9, 1)
+            entry[f"host_slice_v{var}"] = hs
             log(f"[bench] {name} host-slice v{var}: {ms:.2f} ms/call incl. PCIe copies")
         if not args.quick:
             for tname, dt, tdt in (("bf16", fa.DTYPE_BF16, torch.bfloat16), ("f16", fa.DTYPE_F16, torch.float16)):
@@ -351,18 +375,20 @@ def main() -> int:
                                            wl.sk, wl.d, wl.causal, wl.o.data_ptr(), handle)
 
                 steps = auto_steps(torch, call_lp, max(10, args.steps))
-                _, ms = time_calls(torch, call_lp, steps, 2)
-                ent = {"us_per_call": round(ms * 1e3, 1),
-                       "kernels": fa.describe_launch(3, 1, wl.bh, wl.sq, wl.sk, wl.d, wl.causal, dtype=dt)}
+                ms_step, ms = time_calls(torch, call_lp, steps, 2)
+                kernels = fa.describe_launch(3, 1, wl.bh, wl.sq, wl.sk, wl.d, wl.causal, dtype=dt)
+                ent = {"us": round(ms * 1e3, 1)}
                 if kind == "prefill":
                     tf = wl.flops / (ms * 1e-3) / 1e12
-                    ent.update(tflops=round(tf, 1), pct_16bit_mfma_peak=round(100 * tf / PEAK_TFLOPS_16, 1))
+                    ent.update(tflops=round(tf, 1), pct_peak16=round(100 * tf / PEAK_TFLOPS_16, 1))
                 else:
                     lp_bytes = wl.bh * wl.d * (2 * wl.sq + 4 * wl.sk + 4 * wl.sq)   # 16-bit Q, K, V; f32 O
                     gbs = lp_bytes / (ms * 1e-3) / 1e9
-                    ent.update(gbs=round(gbs, 1), pct_hbm_peak=round(100 * gbs / PEAK_GBS, 1))
+                    ent.update(gbs=round(gbs, 1), pct_hbm=round(100 * gbs / PEAK_GBS, 1))
+                counters(ent, kernels, ms)
                 entry[tname] = ent
-                log(f"[bench] {name} {tname}: {ent}")
+                history.append((name, tname, wl, ms_step, ms, ent))
+                log(f"[bench] {name} {tname}: {ent} [{kernels}]")
                 del lq, lk, lv
         configs[name] = entry
         if not args.no_cpu_baseline:
@@ -376,7 +402,7 @@ def main() -> int:
     kernel = kernels.split()[0]
     value = wl.flops / (ms_step * 1e-3) / 1e12
     achieved = wl.flops / (ms_kernel * 1e-3) / 1e12
-    traffic, traffic_note = lookup(traffic_table, kernel, grid_threads(kernels))
+    traffic, traffic_note = trf.lookup(traffic_table, kernel, grid_threads(kernels))
     result = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -396,7 +422,8 @@ def main() -> int:
                    "variant": f"v{args.variant}", "kernel": kernel},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": traffic},
-        "extra": {"configs": configs, "traffic_note": traffic_note, "kernel_source_sha256": kernel_source_hash()},
+        "extra": {"configs": configs, "traffic_note": traffic_note,
+                  "kernel_source_sha256": trf.kernel_source_hash()},
     }
 
     if pending_cpu:
@@ -409,13 +436,15 @@ def main() -> int:
             budget = args.cpu_seconds if name == HEADLINE else args.cpu_seconds_other
             log(f"[bench] cpu baseline {name} ({budget:.1f} s budget, {threads} threads) ...")
             want, sec, n = cpu_v2(inputs, cwl, budget, threads)
-            ent = {"ms_per_call": round(sec * 1e3, 3), "calls": n, "threads": threads, "tier": tier,
-                   "gflops": round(cwl.flops / sec / 1e9, 2)}
+            ent = {"ms": round(sec * 1e3, 3), "calls": n, "threads": threads, "gflops": round(cwl.flops / sec / 1e9, 2)}
             if cwl.kind == "decode":
                 ent["gbs"] = round(cwl.bytes / sec / 1e9, 2)
             configs[name]["cpu_v2"] = ent
-            configs[name]["parity_vs_cpu_v2"] = {f"v{var}": parity(o, want) for var, o in sorted(outs.items())}
-            log(f"[bench] {name} cpu v2: {ent}; parity {configs[name]['parity_vs_cpu_v2']}")
+            par = {f"v{var}": parity(o, want) for var, o in sorted(outs.items())}
+            # [max-abs, rel-L2] per variant; "ok": every variant within the bar
+            configs[name]["parity"] = dict({k: [p["max_abs"], p["rel_l2"]] for k, p in par.items()},
+                                           ok=all(p["within_bar"] for p in par.values()))
+            log(f"[bench] {name} cpu v2: {ent}; parity {par}")
             if name == HEADLINE:
                 result["cpu_baseline"] = {
                     "value": round(cwl.flops / sec / 1e12, 4),
@@ -426,12 +455,74 @@ def main() -> int:
                                f"{sec * 1e3:.1f} ms/call, oracle v2 {tier} tier, Br=64 Bc=128, {threads} threads "
                                f"on {cpu_model()} ({threads} logical CPUs available)"),
                 }
-                p = configs[name]["parity_vs_cpu_v2"][f"v{args.variant}"]
+                p = par[f"v{args.variant}"]
                 result["parity"] = dict(p, vs="oracle v2 on the host, same inputs as the timed calls",
                                         bar={"max_abs": MAX_ABS_TOL, "rel_l2": REL_L2_TOL})
             del want
-    print(json.dumps(result), flush=True)
+        result["extra"]["cpu"] = {"threads": threads, "tier": tier, "model": cpu_model()}
+    if args.csv:
+        append_history(args.csv, history)
+    for line in summary_lines(configs):
+        log(line)
+    print(json.dumps(result, separators=(",", ":")), flush=True)
     return 0
+
+
+def summary_lines(configs: dict) -> list[str]:
+    """One short line per config: per variant us/call, TFLOP/s (GB/s for
+    decode), % of peak (16-bit rows: of the 16-bit peak), MFMA busy % of a
+    prefill kernel where profiled; then the worst max-abs / rel-L2 of the f32
+    variants against CPU v2 and whether all are within the bar."""
+    out = ["[summary] variant us TF|GB/s %peak [mMFMA-busy%] | ... ; worst f32 parity max-abs/rel-L2 vs CPU v2"]
+    for name, e in configs.items():
+        parts = []
+        for var in ("v1", "v2", "v3", "bf16", "f16"):
+            v = e.get(var)
+            if not v:
+                continue
+            if "tflops" in v:
+                rate = f"{v['tflops']:.1f}TF"
+                mb = f" m{v['mfma_busy']:.0f}" if "mfma_busy" in v else ""
+            else:
+                rate, mb = f"{v['gbs']:.0f}GB/s", ""
+            pct = v.get("pct_peak", v.get("pct_peak16", v.get("pct_hbm")))
+            parts.append(f"{var} {v['us']:g}us {rate} {pct:g}%{mb}")
+        par = e.get("parity")
+        ptxt = ""
+        if par:
+            worst = [max(par[k][i] for k in ("v1", "v2", "v3") if k in par) for i in (0, 1)]
+            ptxt = f" ; {worst[0]:.1e}/{worst[1]:.1e} " + ("ok" if par["ok"] else "FAIL")
+        out.append(f"{name}: " + " | ".join(parts) + ptxt)
+    return out
+
+
+def append_history(path: str, history) -> None:
+    """Benchmark-history rows (flash_attention_amd.bench_quick's extended
+    schema): one per config and variant, keyed by the workload name."""
+    from flash_attention_amd import bench_quick as bq
+
+    import torch
+
+    props = torch.cuda.get_device_properties(0)
+    device = (getattr(props, "gcnArchName", "") or props.name).split(":")[0]
+    cus = int(props.multi_processor_count)
+    ts, commit = int(time.time()), bq.resolve_commit()
+    import platform
+
+    rows = []
+    for name, label, wl, ms_wall, ms_kernel, ent in history:
+        rows.append(bq.csv_row(ts, commit, platform.system().lower(), platform.machine(), cus, label, wl.causal,
+                               wl.sq, wl.d, ms_wall, device, ms_kernel, workload=name, seq_len_k=wl.sk,
+                               heads=wl.bh, tflops=ent.get("tflops"),
+                               pct_peak=ent.get("pct_peak", ent.get("pct_peak16")), gbps=ent.get("gbs"),
+                               pct_hbm=ent.get("pct_hbm"), mfma_busy=ent.get("mfma_busy"),
+                               lds_bank_conflicts=ent.get("lds_conflicts"), fetch_gbps=ent.get("fetch_gbs")))
+    new = not os.path.exists(path) or os.path.getsize(path) == 0
+    with open(path, "a", encoding="utf-8") as f:
+        if new:
+            f.write(bq.HEADER_EXT + "\n")
+        f.write("\n".join(rows) + "\n")
+    log(f"[bench] appended {len(rows)} history rows to {path}")
 
 
 if __name__ == "__main__":

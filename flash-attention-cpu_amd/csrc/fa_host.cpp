@@ -436,11 +436,15 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
                 const size_t b = nqb;
                 s_uhead = !causal ? b * nsf
                                   : (b <= bf ? R * (b * (b + 1) / 2) : R * (bf * (bf + 1) / 2) + (b - bf) * nsf);
+                // The kernel keeps unit indices (up to the total plus one
+                // run) in 32 bits: larger totals are refused (AUTO then keeps
+                // the key split; a forced stream split is unsupported).
+                if (s_uhead == 0 || s_uhead > imax || bh > imax / s_uhead) return false;
                 const size_t utot = bh * s_uhead;
                 s_per = std::max<size_t>(4, (utot + want - 1) / want);
                 s_wgs = (utot + s_per - 1) / s_per;
                 s_segs = (max_st + s_per - 1) / s_per + 1;   // most workgroups sharing a block
-                return s_segs <= (size_t)kMaxSplits && s_wgs <= imax && s_uhead <= imax && bh * sq <= imax &&
+                return s_segs <= (size_t)kMaxSplits && utot + s_per <= imax && s_wgs <= imax && bh * sq <= imax &&
                        s_wgs + bh * nqb <= imax;
             };
             // workgroups resident at once: the 16-bit kernels fit two per CU at D <= 128
@@ -1208,22 +1212,29 @@ int fa_release_stream_workspace(void* stream) {
     if (rc != FA_OK) return rc;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     DeviceState& s = g_dev[dev];
-    std::lock_guard<std::mutex> lock(s.ws_mu);
-    auto it = s.ws.find(workspace_key(st));
-    if (it == s.ws.end()) return FA_OK;
+    // Take the stream's buffers out of the table under the lock, then drain
+    // the stream and free them without it, so split calls on other streams
+    // of this device do not wait for this stream.
+    std::vector<void*> bufs;
+    {
+        std::lock_guard<std::mutex> lock(s.ws_mu);
+        auto it = s.ws.find(workspace_key(st));
+        if (it == s.ws.end()) return FA_OK;
+        bufs = std::move(it->second.retired);
+        bufs.push_back(it->second.ptr);
+        s.ws.erase(it);
+    }
     // Work queued on the stream may still use the buffers.
     if (hipStreamSynchronize(st) != hipSuccess) {
         (void)hipGetLastError();
-        return FA_ERR_COPY;
+        return FA_ERR_COPY;   // the buffers stay allocated (never reused) rather than freed under work
     }
     rc = FA_OK;
-    it->second.retired.push_back(it->second.ptr);
-    for (void* p : it->second.retired)
+    for (void* p : bufs)
         if (p && hipFree(p) != hipSuccess) {
             (void)hipGetLastError();
             rc = FA_ERR_ALLOC;
         }
-    s.ws.erase(it);
     return rc;
 }
 

@@ -8,11 +8,15 @@ never compared by accident; with no arguments the last two distinct commits
 compared, otherwise two commit prefixes.  A change of 3 % or more is marked
 ``faster`` / ``SLOWER``.
 
-Accepts both the reference's 10-column rows (device "cpu", no device_ms) and
-the 12-column rows bench_quick --csv writes; repeated header lines are
-skipped (concatenated CSVs), malformed rows are reported and skipped.  For
-GPU rows both timings are compared: time_ms (host-slice call) and device_ms
-(kernels only).
+Accepts the reference's 10-column rows (device "cpu", no device_ms), the
+12-column GPU rows and the 22-column rows with GPU columns that
+bench_quick --csv and bench.py --csv write (the workload name, key length
+and slice count join the key, so bench.py's BASELINE configurations are
+compared config by config; their TFLOP/s or GB/s are shown next to the
+timings); repeated header lines are skipped (concatenated CSVs), malformed
+rows are reported and skipped.  For GPU rows both timings are compared:
+time_ms (host-slice call for bench_quick rows, wall time of a
+device-resident call for bench.py rows) and device_ms (kernels only).
 
 Run: ``python -m flash_attention_amd.bench_compare [--file history.csv] [old new]``.
 """
@@ -37,6 +41,13 @@ class Key:
     causal: bool
     seq_len: int
     d_head: int
+    workload: str = ""
+    seq_len_k: int = 0    # 0: seq_len (a square shape)
+    heads: int = 1
+
+    def __post_init__(self):
+        if self.seq_len_k == 0:
+            object.__setattr__(self, "seq_len_k", self.seq_len)
 
 
 @dataclass
@@ -45,6 +56,7 @@ class Row:
     key: Key
     time_ms: float
     device_ms: float | None
+    rate: str = ""        # "127.1TF" / "6620GB/s" from the GPU columns, when present
 
 
 def _bool(s: str) -> bool:
@@ -61,14 +73,23 @@ def parse_csv(text: str, warn=lambda msg: print(msg, file=sys.stderr)) -> list[R
         if not line or line.startswith("timestamp,"):
             continue
         f = line.split(",")
-        if len(f) not in (10, 12):
+        if len(f) not in (10, 12, 22):
             warn(f"skipping malformed row: {line}")
             continue
         try:
-            device = f[10] if len(f) == 12 else "cpu"
-            device_ms = float(f[11]) if len(f) == 12 else None
-            key = Key(f[2], f[3], device, int(f[4]), f[5], _bool(f[6]), int(f[7]), int(f[8]))
-            rows.append(Row(f[1], key, float(f[9]), device_ms))
+            device = f[10] if len(f) >= 12 else "cpu"
+            device_ms = float(f[11]) if len(f) >= 12 else None
+            seq_len = int(f[7])
+            workload, seq_len_k, heads, rate = "", seq_len, 1, ""
+            if len(f) == 22:
+                workload, seq_len_k, heads = f[12], int(f[13]), int(f[14])
+                if f[15] and not f[17]:
+                    rate = f"{float(f[15]):.1f}TF"
+                elif f[17]:
+                    rate = f"{float(f[17]):.0f}GB/s"
+            key = Key(f[2], f[3], device, int(f[4]), f[5], _bool(f[6]), seq_len, int(f[8]), workload,
+                      seq_len_k, heads)
+            rows.append(Row(f[1], key, float(f[9]), device_ms, rate))
         except ValueError:
             warn(f"skipping malformed row: {line}")
     return rows
@@ -104,6 +125,8 @@ def compare(rows: list[Row], old: str, new: str) -> tuple[list[str], int, int]:
     only_old = only_new = 0
     for key in sorted(set(old_map) | set(new_map)):
         target = f"{key.os}/{key.arch}" + ("" if key.device == "cpu" else f"/{key.device}")
+        if key.workload:
+            target += f" {key.workload}"
         head = (f"{target:<16} {key.threads:>5} {key.variant:>5} {str(key.causal).lower():>6} {key.seq_len:>5} "
                 f"{key.d_head:>5} |")
         o, n = old_map.get(key), new_map.get(key)
@@ -112,8 +135,10 @@ def compare(rows: list[Row], old: str, new: str) -> tuple[list[str], int, int]:
             line = f"{head} {o.time_ms:>10.4f} {n.time_ms:>10.4f} {pct:>+7.1f}% {mark:<6} |"
             if o.device_ms is not None and n.device_ms is not None:
                 dp, dm = _change(o.device_ms, n.device_ms)
-                line += f" {o.device_ms:>10.4f} {n.device_ms:>10.4f} {dp:>+7.1f}% {dm}"
-            lines.append(line)
+                line += f" {o.device_ms:>10.4f} {n.device_ms:>10.4f} {dp:>+7.1f}% {dm:<6}"
+            if o.rate or n.rate:
+                line += f" | {o.rate or '-'} -> {n.rate or '-'}"
+            lines.append(line.rstrip())
         elif n:
             only_new += 1
             dev = f" {'-':>10} {n.device_ms:>10.4f}" if n.device_ms is not None else ""

@@ -15,6 +15,14 @@ counters on a plain device copy of known size:
 ``--trace <dir>`` prints per-launch-size kernel durations of a
 ``rocprofv3 --kernel-trace`` run as a markdown table.
 
+``--pmc-a <dir> --pmc-b <dir> --out profiles/pmc.json`` builds the per-kernel
+counter table (MFMA busy %, non-MFMA VALU per MFMA, wait share, LDS bank
+conflicts) from two rocprofv3 ``--pmc`` runs over bench.py, one per counter
+pass (PMC_PASS_A, PMC_PASS_B below):
+
+    rocprofv3 --pmc <PMC_PASS_A> -d <dir_a> -o run -f csv -- python3 bench.py --no-cpu-baseline --steps 3 --warmup 1
+    rocprofv3 --pmc <PMC_PASS_B> -d <dir_b> -o run -f csv -- python3 bench.py --no-cpu-baseline --steps 3 --warmup 1
+
 Entries are keyed by kernel name and launch size (threads in the grid), so
 the same kernel on two workloads keeps two figures, and each entry carries a
 hash of the kernel sources it was measured on: bench.py reports a figure only
@@ -98,9 +106,85 @@ def build_table(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_mib, 
             "kernel": name, "grid_threads": grid, "dispatches": [nf, nw],
             "fetch_kib_raw": round(f_kib, 1), "write_kib_raw": round(w_kib, 1),
             "fetch_scale": round(fs, 4), "write_scale": round(ws, 4),
+            "fetch_bytes_per_launch": int(round(f_kib * fs * 1024)),
             "hbm_bytes_per_launch": int(round(f_kib * fs * 1024 + w_kib * ws * 1024)),
             "kernel_source_sha256": src,
         }
+    return table
+
+
+# PMC passes behind the per-kernel counter table (each pass in a run of its
+# own: one rocprofv3 --pmc run may hold at most 8 SQ and 2 GRBM counters).
+PMC_PASS_A = ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CYCLES", "SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_WAVE_CYCLES",
+              "SQ_WAIT_INST_ANY", "GRBM_GUI_ACTIVE")
+PMC_PASS_B = ("SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_INSTS_LDS", "SQ_WAIT_INST_LDS", "SQ_LDS_ADDR_CONFLICT",
+              "GRBM_GUI_ACTIVE")
+SIMDS = 1024   # MI355X: 256 CUs x 4 SIMDs
+XCDS = 8
+
+
+def all_counter_means(run_dir: str, prefix: str = "fa_") -> dict[tuple[str, int], dict[str, float]]:
+    """{(kernel name, grid threads): {counter: mean per dispatch}} over a run's CSV files."""
+    sums: dict[tuple[str, int, str], list[float]] = defaultdict(lambda: [0.0, 0])
+    paths = glob.glob(os.path.join(run_dir, "**", "*counter_collection.csv"), recursive=True)
+    if not paths:
+        raise FileNotFoundError(f"no *counter_collection.csv under {run_dir}")
+    csv.field_size_limit(1 << 24)
+    for path in paths:
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                if not row["Kernel_Name"].startswith(prefix):
+                    continue
+                k = (row["Kernel_Name"], int(row["Grid_Size"]), row["Counter_Name"])
+                sums[k][0] += float(row["Counter_Value"])
+                sums[k][1] += 1
+    out: dict[tuple[str, int], dict[str, float]] = {}
+    for (name, grid, ctr), (s, n) in sums.items():
+        out.setdefault((name, grid), {})[ctr] = s / n
+        out[(name, grid)].setdefault("_dispatches", n)
+    return out
+
+
+def pmc_figures(a: dict[str, float], b: dict[str, float]) -> dict:
+    """Derived figures of one kernel launch size from the two passes' means.
+
+    mfma_busy_pct: SQ_VALU_MFMA_BUSY_CYCLES (summed over the SIMDs) over the
+    SIMD-cycles the GPU was active (GRBM_GUI_ACTIVE summed over the XCDs / 8
+    per XCD x 1024 SIMDs); valu_per_mfma: non-MFMA VALU instructions per MFMA;
+    wait_pct: SQ_WAIT_INST_ANY share of the wave cycles; lds_bank_conflicts:
+    SQ_LDS_BANK_CONFLICT cycles per launch, and their share of the LDS
+    unit's active cycles."""
+    active = a["GRBM_GUI_ACTIVE"] / XCDS
+    mfma = a.get("SQ_INSTS_MFMA", 0.0)
+    valu = a.get("SQ_INSTS_VALU", 0.0)
+    fig = {
+        "gui_active_cycles_per_xcd": int(round(active)),
+        "mfma_busy_pct": round(100.0 * a["SQ_VALU_MFMA_BUSY_CYCLES"] / (active * SIMDS), 1) if active else None,
+        "mfma_insts": int(round(mfma)),
+        "valu_per_mfma": round((valu - mfma) / mfma, 2) if mfma else None,
+        "valu_insts_non_mfma": int(round(valu - mfma)),
+        "wait_pct": round(100.0 * a["SQ_WAIT_INST_ANY"] / a["SQ_WAVE_CYCLES"], 1) if a.get("SQ_WAVE_CYCLES") else None,
+        "lds_bank_conflicts": int(round(b.get("SQ_LDS_BANK_CONFLICT", 0.0))),
+        "lds_conflict_pct": (round(100.0 * b["SQ_LDS_BANK_CONFLICT"] / b["SQ_LDS_IDX_ACTIVE"], 2)
+                             if b.get("SQ_LDS_IDX_ACTIVE") else 0.0),
+        "lds_insts": int(round(b.get("SQ_INSTS_LDS", 0.0))),
+        "dispatches": [int(a.get("_dispatches", 0)), int(b.get("_dispatches", 0))],
+    }
+    return fig
+
+
+def build_pmc_table(dir_a: str, dir_b: str, prefix: str = "fa_") -> dict:
+    pa, pb = all_counter_means(dir_a, prefix), all_counter_means(dir_b, prefix)
+    src = kernel_source_hash()
+    table = {}
+    for key in sorted(set(pa) & set(pb)):
+        name, grid = key
+        if "GRBM_GUI_ACTIVE" not in pa[key] or "SQ_VALU_MFMA_BUSY_CYCLES" not in pa[key]:
+            continue
+        ent = {"kernel": name, "grid_threads": grid}
+        ent.update(pmc_figures(pa[key], pb[key]))
+        ent["kernel_source_sha256"] = src
+        table[f"{name}@{grid}"] = ent
     return table
 
 
@@ -137,6 +221,21 @@ def trace_markdown(run_dir: str) -> str:
     return "\n".join(out)
 
 
+def lookup_entry(table_path: str, kernel: str, grid_threads: int):
+    """The table's entry for (kernel, grid) when measured on these kernel sources, else None."""
+    try:
+        with open(table_path) as f:
+            table = json.load(f)
+    except (OSError, ValueError):
+        return None
+    ent = table.get(f"{kernel}@{grid_threads}")
+    if not ent or ent.get("kernel_source_sha256") != kernel_source_hash():
+        return None
+    if "fetch_kib_raw" in ent and "fetch_bytes_per_launch" not in ent:
+        ent["fetch_bytes_per_launch"] = int(round(ent["fetch_kib_raw"] * ent["fetch_scale"] * 1024))
+    return ent
+
+
 def lookup(table_path: str, kernel: str, grid_threads: int):
     """HBM bytes per launch for (kernel, grid), or (None, reason) when absent or measured on other sources."""
     try:
@@ -160,10 +259,21 @@ def main(argv=None) -> int:
     ap.add_argument("--copy-fetch")
     ap.add_argument("--copy-write")
     ap.add_argument("--copy-mib", type=int, default=1024)
+    ap.add_argument("--pmc-a", help="run dir of the first PMC pass (PMC_PASS_A counters)")
+    ap.add_argument("--pmc-b", help="run dir of the second PMC pass (PMC_PASS_B counters)")
     ap.add_argument("--out")
     a = ap.parse_args(argv)
     if a.trace:
         print(trace_markdown(a.trace))
+        return 0
+    if a.pmc_a or a.pmc_b:
+        if not (a.pmc_a and a.pmc_b and a.out):
+            ap.error("--pmc-a, --pmc-b and --out go together")
+        table = build_pmc_table(a.pmc_a, a.pmc_b)
+        with open(a.out, "w") as f:
+            json.dump(table, f, indent=1, sort_keys=True)
+            f.write("\n")
+        print(f"wrote {len(table)} kernel entries to {a.out}")
         return 0
     if not (a.fetch and a.write and a.copy_fetch and a.copy_write and a.out):
         ap.error("--fetch, --write, --copy-fetch, --copy-write and --out are required")

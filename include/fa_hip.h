@@ -17,8 +17,9 @@
  * stream and return as soon as the kernels are queued.
  *
  * Thread safety: every entry point may be called from several threads at
- * once (the crate's functions are Sync).  Host-slice calls on one device
- * are serialised internally.
+ * once (the crate's functions are Sync).  Up to four host-slice calls per
+ * device run concurrently, each on its own stream, device staging buffer and
+ * pinned copy ring; further callers wait until one of those four finishes.
  */
 #ifndef FA_HIP_H
 #define FA_HIP_H
@@ -219,7 +220,9 @@ int fa_device_ex_noalloc(int variant, void* stream, const float* q, const float*
  * in f32, and the probabilities are rounded to the input type for PV (the
  * row sums add up the rounded values), so each output element is within
  * u/(1-u) * max|V| of f32 attention on the same 16-bit inputs (u = 2^-8
- * bf16, 2^-11 f16).  Causal masking, shape checks and
+ * bf16, 2^-11 f16; f16 probabilities are rounded as 2^7 p, so only those
+ * below 2^-21 of the row's reference fall below f16's normal range, adding
+ * at most n * 2^-32 * max|V| over a row of n keys).  Causal masking, shape checks and
  * zero-dimension behaviour are those of fa_multihead_v2; d_head <= 256.  The
  * algorithm is v2/v3's (deferred normalisation, causal skip); no variant
  * argument.  opts: softmax_scale, path and num_splits as for fa_device_ex;
@@ -249,8 +252,11 @@ int fa_naive_attention(const float* q, size_t q_len, const float* k, size_t k_le
  * caller's stream).  precision FA_NAIVE_F64 computes scores, softmax and PV
  * in f64 (output rounded to f32): an on-device reference for checking the
  * flash kernels at sizes a CPU oracle cannot reach.  The score buffer is
- * allocated stream-ordered, at most 8 GiB at a time (heads in chunks).  No
- * counterpart beyond naive_attention itself in the reference. */
+ * allocated stream-ordered for as many whole heads at a time as fit in both
+ * 8 GiB and half the device memory free at the call (at least one head); a
+ * single head's score matrix larger than half the free memory returns
+ * FA_ERR_ALLOC with nothing queued.  No counterpart beyond naive_attention
+ * itself in the reference. */
 #define FA_NAIVE_F32 0
 #define FA_NAIVE_F64 1
 int fa_naive_device(void* stream, const float* q, const float* k, const float* v, size_t batch,

@@ -75,3 +75,22 @@ def attention_f64(q, k, v, seq_q, seq_k, d, causal):
     den = p.sum(axis=1, keepdims=True)
     p = np.divide(p, den, out=np.zeros_like(p), where=den > 0)
     return (p @ v).ravel()
+
+
+def long_row_f16_case():
+    """A row of n keys whose probabilities (all but one) equal t ~ 179.5 x 2^-24,
+    inside f16's subnormal range: key 0 scores 48 (q = 4 e0, k0 = 12 e0, scale
+    1/8) and sets the reference, the others score 4 b with b = -10.890625, and
+    n = 1/t so that their total weight equals key 0's.  V row 0 is -1, the
+    others +1, so O = (-1 + n t) / (1 + n t) ~ 0 and any common rounding of t
+    moves O by about half its relative error.  Rounded as a subnormal, t is
+    off by 2.7e-3 (O by 1.4e-3, three times the u/(1-u) bound); rounded as
+    2^7 t, a normal f16, by at most u = 2^-11."""
+    d, sq, n = 64, 16, 93462
+    q = np.zeros((sq, d), np.float16)
+    q[:, 0] = 4.0
+    k = np.zeros((n + 1, d), np.float16)
+    k[0, 0], k[1:, 0] = 12.0, -10.890625
+    v = np.ones((n + 1, d), np.float16)
+    v[0] = -1.0
+    return q.ravel(), k.ravel(), v.ravel(), sq, n + 1, d

@@ -272,6 +272,21 @@ def test_planning_stream_split_prefill():
         "fa_prefill_lp_bf16_d64_2_t1s grid=")
 
 
+def test_planning_stream_split_refuses_unit_totals_past_32_bits():
+    # 2 slices x 3,000,000^2 at d32 has about 2.2e9 key-stage units: the
+    # kernel's 32-bit unit indices would wrap, so the forced stream split is
+    # unsupported (planned on the CPU only; this shape never runs)
+    with pytest.raises(fa.FaError) as e:
+        describe(2, 1, 2, 3_000_000, 3_000_000, 32, False, fa.PATH_STREAM)
+    assert e.value.status == fa.FA_ERR_UNSUPPORTED
+    with pytest.raises(fa.FaError) as e:
+        describe(2, 1, 2, 3_000_000, 3_000_000, 32, False, fa.PATH_STREAM, 1)
+    assert e.value.status == fa.FA_ERR_UNSUPPORTED
+    # a long causal slice well inside the limit (131,406 units) is planned
+    s = describe(2, 1, 1, 46336, 46336, 32, True, fa.PATH_STREAM)
+    assert s.startswith("fa_prefill_v2_d32_1s ")
+
+
 def test_planning_key_split_prefill():
     # config 5c's shape, split forced over 3 workgroups per block
     s = describe(3, 1, 16, 1000, 1000, 256, True, fa.PATH_PREFILL, 3)

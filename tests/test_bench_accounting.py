@@ -89,3 +89,79 @@ def test_bench_rows_have_distinct_launch_keys():
     shared = {k: v for k, v in use.items() if len(v) > 1}
     assert shared == {("fa_prefill_v1_d128_1", 16384): {"config4a", "config4b"}}, shared
 
+
+
+def _fake_configs():
+    """An extra.configs dict shaped as bench.py builds it, every config and variant present."""
+    configs = {}
+    for (name, bh, sq, sk, d, causal, _s, _u, kind) in bench.CONFIGS:
+        e = {"shape": "x" * 60, "flop": bench.flops_of(bh, sq, sk, d, causal), "bytes": bench.bytes_of(bh, sq, sk, d)}
+        for var in ("v1", "v2", "v3"):
+            ent = {"us": 12345.6}
+            if kind == "prefill":
+                ent.update(tflops=123.45, pct_peak=78.5, mfma_busy=81.2, lds_conflicts=0, hbm_mb=199.4,
+                           fetch_gbs=612.3)
+            else:
+                ent.update(gbs=6620.4, pct_hbm=82.8, hbm_mb=1074.2, fetch_gbs=6600.1, mfma_busy=3.1,
+                           lds_conflicts=0)
+            e[var] = ent
+        if name in ("config2", "config3", "config4a", "config5"):
+            for t in ("bf16", "f16"):
+                e[t] = {"us": 46.2, "tflops": 744.1, "pct_peak16": 29.8, "mfma_busy": 29.5, "lds_conflicts": 0}
+        e["cpu_v2"] = {"ms": 23800.123, "calls": 200, "threads": 16, "gflops": 1444.44}
+        e["parity"] = {"v1": [1.19e-6, 5.75e-7], "v2": [1.19e-6, 5.75e-7], "v3": [1.19e-6, 5.75e-7], "ok": True}
+        configs[name] = e
+    return configs
+
+
+def test_summary_survives_a_2000_character_tail():
+    """The driver keeps the last few KB of stderr: the closing summary (one
+    line per config, every variant with time, rate, % of peak and parity)
+    must fit in 2000 characters."""
+    lines = bench.summary_lines(_fake_configs())
+    text = "\n".join(lines)
+    assert len(lines) == 1 + len(bench.CONFIGS)
+    assert len(text) < 2000, len(text)
+    c2 = next(line for line in lines if line.startswith("config2:"))
+    assert "v3 12345.6us 123.5TF 78.5% m81" in c2 and "bf16 46.2us 744.1TF 29.8% m30" in c2
+    assert c2.endswith("; 1.2e-06/5.8e-07 ok")
+    c4 = next(line for line in lines if line.startswith("config4a:"))
+    assert "v2 12345.6us 6620GB/s 82.8% |" in c4
+
+
+def test_json_line_stays_compact():
+    """The one stdout JSON line (every config's figures in extra.configs) stays
+    well inside the driver's 16 KB stdout tail."""
+    import json as _json
+    line = _json.dumps({"metric": bench.METRIC, "extra": {"configs": _fake_configs()}}, separators=(",", ":"))
+    assert len(line) < 9000, len(line)
+
+
+def test_pmc_table_from_counter_runs(tmp_path):
+    """build_pmc_table joins the two PMC passes per (kernel, launch size) and
+    derives MFMA busy %, VALU per MFMA, wait share and LDS conflicts."""
+    hdr = "Kernel_Name,Grid_Size,Counter_Name,Counter_Value\n"
+    a = tmp_path / "a" / "x"
+    b = tmp_path / "b" / "x"
+    a.mkdir(parents=True)
+    b.mkdir(parents=True)
+    rows_a = [("SQ_VALU_MFMA_BUSY_CYCLES", 553648128), ("SQ_INSTS_MFMA", 17301504), ("SQ_INSTS_VALU", 23087104),
+              ("SQ_WAVE_CYCLES", 322.0e6), ("SQ_WAIT_INST_ANY", 190.8e6), ("GRBM_GUI_ACTIVE", 5327934),
+              ("SQ_BUSY_CYCLES", 1.0)]
+    rows_b = [("SQ_LDS_BANK_CONFLICT", 0), ("SQ_LDS_IDX_ACTIVE", 17301504), ("SQ_INSTS_LDS", 4325376),
+              ("GRBM_GUI_ACTIVE", 5327934)]
+    (a / "run_counter_collection.csv").write_text(
+        hdr + "".join(f"fa_k,131072,{c},{v}\n" for c, v in rows_a) + "other_kernel,64,GRBM_GUI_ACTIVE,5\n")
+    (b / "run_counter_collection.csv").write_text(hdr + "".join(f"fa_k,131072,{c},{v}\n" for c, v in rows_b))
+    table = traffic.build_pmc_table(str(tmp_path / "a"), str(tmp_path / "b"))
+    assert list(table) == ["fa_k@131072"]
+    e = table["fa_k@131072"]
+    # 553.6 M busy cycles over (5,327,934 / 8 XCDs) x 1024 SIMDs
+    assert e["mfma_busy_pct"] == pytest.approx(81.2, abs=0.05)
+    assert e["valu_per_mfma"] == pytest.approx((23087104 - 17301504) / 17301504, abs=0.005)
+    assert e["wait_pct"] == pytest.approx(59.3, abs=0.05)
+    assert e["lds_bank_conflicts"] == 0 and e["kernel_source_sha256"] == traffic.kernel_source_hash()
+    path = tmp_path / "pmc.json"
+    path.write_text(json.dumps(table))
+    assert traffic.lookup_entry(str(path), "fa_k", 131072)["mfma_busy_pct"] == e["mfma_busy_pct"]
+    assert traffic.lookup_entry(str(path), "fa_k", 64) is None

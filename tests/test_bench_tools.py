@@ -118,11 +118,67 @@ def test_bench_quick_csv_end_to_end(tmp_path):
     with redirect_stdout(buf):
         assert bq.main(["--csv", "--iters", "2", "--dev-iters", "3"]) == 0
     lines = buf.getvalue().strip().splitlines()
-    assert lines[0] == bq.HEADER and len(lines) == 1 + len(bq.SHAPES) * len(bq.RUNS)
+    assert lines[0] == bq.HEADER_EXT and len(lines) == 1 + len(bq.SHAPES) * len(bq.RUNS)
     rows = bc.parse_csv(buf.getvalue(), warn=lambda m: pytest.fail(m))
     assert all(r.time_ms > 0 and r.device_ms > 0 and r.key.threads > 0 for r in rows)
+    for line in lines[1:]:   # the GPU columns: algorithmic TFLOP/s and GB/s are always filled
+        f = line.split(",")
+        assert len(f) == 22 and f[12] == "" and float(f[15]) > 0 and float(f[17]) > 0, line
     # fed back twice under two commits, everything joins
     c1 = buf.getvalue().replace(f",{rows[0].commit},", ",old0001,")
     c2 = buf.getvalue().replace(f",{rows[0].commit},", ",new0002,")
     lines, only_old, only_new = bc.compare(bc.parse_csv(c1 + c2), "old0001", "new0002")
     assert only_old == 0 and only_new == 0 and len(lines) == 3 + len(rows)
+
+
+def _ext_row(commit, workload, variant, sq, sk, heads, d, wall, dev, **cols):
+    return bq.csv_row(1800000000, commit, "linux", "x86_64", 256, variant, True, sq, d, wall, "gfx950", dev,
+                      workload=workload, seq_len_k=sk, heads=heads, **cols)
+
+
+def test_extended_row_schema_and_gpu_columns():
+    assert bq.HEADER_EXT.split(",")[:12] == bq.HEADER.split(",")
+    assert bq.HEADER_EXT.split(",")[12:] == ["workload", "seq_len_k", "heads", "tflops", "pct_peak", "gbps",
+                                             "pct_hbm", "mfma_busy", "lds_bank_conflicts", "fetch_gbps"]
+    row = _ext_row("abc1234", "config2", "v3", 2048, 2048, 32, 128, 0.2712, 0.2704, tflops=127.1234,
+                   pct_peak=80.81, mfma_busy=81.2, lds_bank_conflicts=0, fetch_gbps=612.34)
+    assert row.split(",")[12:] == ["config2", "2048", "32", "127.123", "80.8", "", "", "81.2", "0", "612.3"]
+    (r,) = bc.parse_csv(bq.HEADER_EXT + "\n" + row)
+    assert r.key == bc.Key("linux", "x86_64", "gfx950", 256, "v3", True, 2048, 128, "config2", 2048, 32)
+    assert r.rate == "127.1TF" and r.device_ms == pytest.approx(0.2704)
+    dec = _ext_row("abc1234", "config4a", "v2", 1, 32768, 32, 128, 0.17, 0.16, gbps=6620.4, pct_hbm=82.8)
+    (r,) = bc.parse_csv(dec)
+    assert r.rate == "6620GB/s" and r.key.seq_len_k == 32768
+    with pytest.raises(TypeError):
+        bq.csv_row(1, "c", "linux", "x86_64", 1, "v1", False, 1, 1, 1.0, "gfx950", 1.0, bogus=1)
+
+
+def test_gpu_columns_of_a_quick_row():
+    # 1024^2 d64 non-causal in 0.1 ms: 4 * 64 * 1024^2 FLOP, 4 * 64 * 4 * 1024 bytes
+    cols = bq.gpu_columns(0, 1024, 64, False, 0.1)
+    assert cols["tflops"] == pytest.approx(4 * 64 * 1024 ** 2 / 1e-4 / 1e12)
+    assert cols["pct_peak"] == pytest.approx(100 * cols["tflops"] / 157.3)
+    assert cols["gbps"] == pytest.approx(4 * 64 * 4 * 1024 / 1e-4 / 1e9)
+    causal = bq.gpu_columns(0, 1024, 64, True, 0.1)
+    assert causal["tflops"] == pytest.approx(cols["tflops"] * 1025 / 2048)
+
+
+def test_compare_keeps_workloads_apart_and_mixes_row_forms():
+    rows = bc.parse_csv("\n".join([
+        bq.HEADER,
+        _gpu_row("aaa1111", "v2", True, 2048, 128, 3.0, 0.30),           # 12-column quick row
+        bq.HEADER_EXT,
+        _ext_row("aaa1111", "config2", "v2", 2048, 2048, 32, 128, 0.29, 0.29, tflops=118.0),
+        _ext_row("aaa1111", "config3", "v2", 16384, 16384, 8, 128, 4.3, 4.3, tflops=127.0),
+        _ext_row("bbb2222", "", "v2", 2048, 2048, 1, 128, 2.7, 0.27, tflops=20.0),   # same quick key
+        _ext_row("bbb2222", "config2", "v2", 2048, 2048, 32, 128, 0.25, 0.25, tflops=137.0),
+        _ext_row("bbb2222", "config3", "v2", 16384, 16384, 8, 128, 4.5, 4.5, tflops=122.0),
+    ]))
+    lines, only_old, only_new = bc.compare(rows, "aaa1111", "bbb2222")
+    assert only_old == 0 and only_new == 0
+    c2 = next(line for line in lines if "config2" in line)
+    assert "-13.8% faster" in c2 and "118.0TF -> 137.0TF" in c2
+    c3 = next(line for line in lines if "config3" in line)
+    assert "SLOWER" in c3
+    quick = [line for line in lines if "gfx950 " in line and "config" not in line]
+    assert len(quick) == 1 and "-10.0% faster" in quick[0]

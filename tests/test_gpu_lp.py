@@ -9,7 +9,10 @@ same MFMA.  With w_j = p_j / l the output moves by
 |sum_j w_j d_j (v_j - o)| / (1 + sum_j w_j d_j) <= u/(1-u) * sum_j w_j |v_j - o|
 <= u/(1-u) * max|V| (o is the w-weighted mean of the v_j, and a mean absolute
 deviation about the mean of values in [-M, M] is at most M).  The bar:
-max-abs <= u/(1-u) * max|V| + 2e-5 and relative L2 <= u.  Known answers that
+max-abs <= u/(1-u) * max|V| + 2e-5 and relative L2 <= u.  (f16 rounds
+2^7 p_j, so |d_j| <= u holds down to p_j = 2^-21 of the row's reference;
+below that the absolute error, at most 2^-32 per key against row sums of at
+least 1, stays under the 2e-5 slack for rows of up to 85,000 such keys.)  Known answers that
 involve no rounding (a row that sees one key returns that key's V row) are
 checked bit for bit.
 """
@@ -20,7 +23,7 @@ import pytest
 
 import flash_attention_amd as fa
 import oracle
-from fa_testutil import max_abs_diff, normal_vec, rel_l2, uniform_vec
+from fa_testutil import long_row_f16_case, max_abs_diff, normal_vec, rel_l2, uniform_vec
 
 pytestmark = pytest.mark.gpu
 
@@ -137,6 +140,28 @@ def test_lp_known_answers_are_exact(dtype):
     out1 = lp_device(dtype, q16, k16[:bh * d].copy(), v16[:bh * d].copy(), bh, s, 1, d, False).reshape(bh, s, d)
     for h in range(bh):   # head h's single key/value row is element block h of the first bh*d
         assert np.array_equal(out1[h], np.tile(v32[h * d:(h + 1) * d], (s, 1)))
+
+
+def test_lp_f16_long_row_of_small_probabilities():
+    """The f16 prefill on the long row of fa_testutil.long_row_f16_case, every
+    key in one workgroup (forced prefill, no key split: a split not holding
+    key 0 would take one of the small keys as its reference), against exact
+    attention in float64 on the widened inputs, max-abs under u/(1-u) *
+    max|V| + 2e-5 (O is near 0, so no relative bar).  Not against the CPU v2
+    oracle: its f32 running sums add t ~ 179.5 ulp(1) once per key and round
+    the same way every time, which leaves CPU v2 6.7e-4 off here."""
+    q16, k16, v16, sq, sk, d = long_row_f16_case()
+    q, k, v = (a.astype(np.float64).reshape(-1, d) for a in (q16, k16, v16))
+    s = q @ k.T / 8.0                                  # scale 1/sqrt(64)
+    p = np.exp(s - s.max(axis=1, keepdims=True))
+    want = ((p @ v) / p.sum(axis=1, keepdims=True)).ravel()
+    print("[case] f16 long row", fa.describe_launch(3, 1, 1, sq, sk, d, False, fa.PATH_PREFILL, dtype=fa.DTYPE_F16),
+          flush=True)
+    got = lp_device(fa.DTYPE_F16, q16, k16, v16, 1, sq, sk, d, False, path=fa.PATH_PREFILL)
+    tol = lp_bound(fa.DTYPE_F16, v16.astype(np.float32))
+    ma = float(np.max(np.abs(got.astype(np.float64) - want)))
+    print(f"[lp-parity] f16 long row: max-abs {ma:.3g} against float64 (bound {tol:.3g})", flush=True)
+    assert ma <= tol, (ma, tol)
 
 
 @pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16])

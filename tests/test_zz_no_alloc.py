@@ -69,6 +69,51 @@ PAIRS = [
 ]
 
 
+def test_noalloc_allocates_nothing_on_a_fresh_stream():
+    """Two no-alloc calls (a 48 MiB key-split plan, then a smaller one) on a
+    stream no fa_device_ex call has used leave the device's free memory
+    exactly as it was; the same plan through fa_device_ex on another fresh
+    stream does allocate its workspace (the positive control).  Inputs and
+    outputs are allocated, and each stream's first use (torch fills on it)
+    made, before the free memory is read."""
+    torch = _torch()
+    fa.init()
+    cases = [PAIRS[2][0], PAIRS[2][1]]
+    data = []
+    for i, (variant, bh, sq, sk, d, causal, path, splits) in enumerate(cases):
+        t = _tensors(bh, sq, sk, d, 600 + i)
+        data.append((t, torch.empty(bh * sq * d, device=t[0].device), torch.empty(bh * sq * d, device=t[0].device)))
+    torch.cuda.synchronize()
+
+    def run(fn, stream, which):
+        for (variant, bh, sq, sk, d, causal, path, splits), (t, o_na, o_ex) in zip(cases, data):
+            out = o_na if which == "na" else o_ex
+            fn(variant, t[0].data_ptr(), t[1].data_ptr(), t[2].data_ptr(), 1, bh, sq, sk, d, causal, out.data_ptr(),
+               stream.cuda_stream, path=path, num_splits=splits)
+        stream.synchronize()
+
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for s in (s1, s2):
+        with torch.cuda.stream(s):
+            for _t, o_na, o_ex in data:
+                o_na.fill_(7.0)
+                o_ex.fill_(7.0)
+        s.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    run(fa.attention_device_noalloc, s1, "na")
+    free1 = torch.cuda.mem_get_info()[0]
+    print(f"[no-alloc] free device memory {free0} -> {free1} across two no-alloc calls", flush=True)
+    assert free1 == free0
+    ws = _workspace(*cases[0])
+    run(fa.attention_device, s2, "ex")
+    free2 = torch.cuda.mem_get_info()[0]
+    print(f"[no-alloc] fa_device_ex on a fresh stream: free {free1} -> {free2} (workspace {ws})", flush=True)
+    assert free1 - free2 >= ws
+    fa.release_stream_workspace(s2.cuda_stream)
+    for (_t, o_na, o_ex), case in zip(data, cases):
+        assert np.array_equal(o_na.cpu().numpy(), o_ex.cpu().numpy()), case
+
+
 @pytest.mark.parametrize("first,second", PAIRS)
 def test_noalloc_matches_fa_device_ex_on_two_calls(first, second):
     fa.init()
