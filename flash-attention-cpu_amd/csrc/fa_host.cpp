@@ -290,9 +290,8 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     const int dtype = opts ? opts->dtype : FA_DTYPE_F32;
     if (dtype != FA_DTYPE_F32 && dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F16) return FA_ERR_INVALID_ARG;
     const bool lp = dtype != FA_DTYPE_F32;   // 16-bit inputs: the fa_prefill_lp kernels
+    if (lp && variant == 1) return FA_ERR_INVALID_ARG;   // the 16-bit kernels run v2/v3's algorithm
     if (path < FA_PATH_AUTO || path > FA_PATH_STREAM) return FA_ERR_INVALID_ARG;
-    if ((path == FA_PATH_SPLITKV || path == FA_PATH_SPLITKV_ROWS || path == FA_PATH_STREAM) && variant == 1)
-        return FA_ERR_INVALID_ARG;
     if (opts && opts->num_splits < 0) return FA_ERR_INVALID_ARG;
     if (d > (size_t)kMaxD) return FA_ERR_UNSUPPORTED;
     // d_head > 256: f32 prefill kernels only (column groups; key split allowed)
@@ -318,6 +317,10 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     p.d = static_cast<int>(d);
     p.causal = causal ? 1 : 0;
     p.scale_log2e = scale * 1.44269504088896341f;
+    // v1 visits every key of every query block (no causal skip,
+    // src/v1.rs:209-216): its splits count each block's keys as all seq_k.
+    p.full_keys = variant == 1 ? 1 : 0;
+    const bool causal_skip = causal && variant != 1;
 
     const size_t rows = (size_t)(lp ? fa_lp_rows() : fa_prefill_rows(D));   // query rows per prefill workgroup
     const size_t nqb = (sq + rows - 1) / rows;
@@ -337,7 +340,7 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     // the 16-bit prefill, 45.9 against 104.7 us).
     const bool step_shape = sq <= 2 * (size_t)kDecodeRows && (!lp || rows_ok);
     bool split = false;
-    if (variant != 1) {
+    {   // every variant: v1's split kernels keep its per-block normalisation
         if (path == FA_PATH_SPLITKV || path == FA_PATH_SPLITKV_ROWS) {
             split = true;
         } else if (path == FA_PATH_AUTO && !wide && step_shape) {
@@ -409,10 +412,10 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
         // splits beats several rounds of short ones.  The grid lists only
         // workgroups with keys.
         size_t per = 0;
-        if (variant != 1 || lp) {
+        {
             const size_t SKs = (size_t)(lp ? fa_lp_stage_keys() : fa_prefill_stage_keys(D, variant));
             auto block_stages = [&](size_t b) {
-                const size_t kend = causal ? std::min(sk, (b + 1) * rows) : sk;
+                const size_t kend = causal_skip ? std::min(sk, (b + 1) * rows) : sk;
                 return (kend + SKs - 1) / SKs;
             };
             const size_t max_st = block_stages(nqb - 1);   // causal key ends grow with the block
@@ -434,8 +437,8 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
             auto stream_fit = [&](size_t want) -> bool {
                 const size_t R = rows / SKs, nsf = (sk + SKs - 1) / SKs, bf = sk / rows;
                 const size_t b = nqb;
-                s_uhead = !causal ? b * nsf
-                                  : (b <= bf ? R * (b * (b + 1) / 2) : R * (bf * (bf + 1) / 2) + (b - bf) * nsf);
+                s_uhead = !causal_skip ? b * nsf
+                                       : (b <= bf ? R * (b * (b + 1) / 2) : R * (bf * (bf + 1) / 2) + (b - bf) * nsf);
                 // The kernel keeps unit indices (up to the total plus one
                 // run) in 32 bits: larger totals are refused (AUTO then keeps
                 // the key split; a forced stream split is unsupported).
@@ -450,7 +453,7 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
             // workgroups resident at once: the 16-bit kernels fit two per CU at D <= 128
             const size_t resident = (size_t)num_cus * (lp && D <= 128 ? 2 : 1);
             bool stream = false;
-            if (path == FA_PATH_STREAM) {   // v2/v3 (checked above)
+            if (path == FA_PATH_STREAM) {
                 if (opts->num_splits > 0 && (size_t)opts->num_splits > imax) return FA_ERR_UNSUPPORTED;
                 if (!stream_fit(opts->num_splits > 0 ? (size_t)opts->num_splits : resident)) return FA_ERR_UNSUPPORTED;
                 stream = true;
@@ -533,7 +536,8 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
                 p.merge_scale = 1.0f;   // prefill partial maxima are in the log2 domain
                 p.pair_w = 0;           // the compact split grid has its own order
                 size_t wgs = 0;   // compact grid: split y of every block that reaches it
-                for (size_t y = 0; y < nks; ++y) wgs += (causal ? nqb - std::min(nqb, y * per * SKs / rows) : nqb) * bh;
+                for (size_t y = 0; y < nks; ++y)
+                    wgs += (causal_skip ? nqb - std::min(nqb, y * per * SKs / rows) : nqb) * bh;
                 if (wgs > imax) return FA_ERR_UNSUPPORTED;
                 plan->first.gx = static_cast<unsigned>(wgs);
                 std::snprintf(buf, sizeof(buf), "fa_merge_d%d", D);
@@ -577,12 +581,14 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     p.num_splits = static_cast<int>(nsplit);
     p.split_len = static_cast<int>(split_len);
     p.merge_scale = p.scale_log2e;   // decode partial maxima are raw scores
+    // v1: the instantiations with its per-block normalisation ("_v1")
+    const char* v1tag = variant == 1 ? "v1_" : "";
     if (row_decode) {
         const int rq = sq <= 1 ? 1 : (sq <= 2 ? 2 : 4);
         if (lp)
             std::snprintf(buf, sizeof(buf), "fa_decode_rows_%s_d%d_q1", dtype == FA_DTYPE_BF16 ? "bf16" : "f16", D);
         else
-            std::snprintf(buf, sizeof(buf), "fa_decode_rows_d%d_q%d", D, rq);
+            std::snprintf(buf, sizeof(buf), "fa_decode_rows_%sd%d_q%d", v1tag, D, rq);
     } else if (lp) {
         // 16-bit K/V streamed and widened in registers: 8-byte loads need d % 4 == 0
         const bool vec8 = (d % 4 == 0) && aligned8(q) && aligned8(k) && aligned8(v) && aligned16(out);
@@ -590,7 +596,7 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
                       vec8 ? 1 : 0);
     } else {
         // 0: scalar loads, 1: 16-byte loads, 2: K through per-wave LDS rings (D = 64, 128)
-        std::snprintf(buf, sizeof(buf), "fa_decode_d%d_%d", D, vec ? (D == 64 || D == 128 ? 2 : 1) : 0);
+        std::snprintf(buf, sizeof(buf), "fa_decode_%sd%d_%d", v1tag, D, vec ? (D == 64 || D == 128 ? 2 : 1) : 0);
     }
     plan->first.name = buf;
     plan->first.gx = static_cast<unsigned>(nsplit * nqt * bh);   // split-fastest, then tile, then slice

@@ -203,12 +203,13 @@ __device__ __forceinline__ void map_pair(const FaParams& p, int x, int& qa, int&
 // process (a grid padded with idle workgroups lets the dispatcher queue
 // working ones behind busy CUs).  Row y holds split y of every query block
 // whose key range reaches y * split_len -- causal blocks qb >= floor(y *
-// split_len / ks_rows), all blocks otherwise -- in map_block's order.
+// split_len / ks_rows), all blocks otherwise (and for v1, whose blocks all
+// visit every key) -- in map_block's order.
 __device__ __forceinline__ void map_block_split(const FaParams& p, int& qb, int& bh, int& y) {
     int t = blockIdx.x;
     int cnt = p.nqb;
     for (y = 0;; ++y) {
-        cnt = p.causal ? p.nqb - (int)(((long long)y * p.split_len) / p.ks_rows) : p.nqb;
+        cnt = (p.causal && !p.full_keys) ? p.nqb - (int)(((long long)y * p.split_len) / p.ks_rows) : p.nqb;
         if (t < cnt * p.bh || y + 1 >= p.num_splits) break;
         t -= cnt * p.bh;
     }
@@ -971,8 +972,10 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
     } else {
         // Single LDS stage; the next stage's global loads are issued into
         // registers before the current stage computes (D = 1024: its 64
-        // registers would spill, so each stage is loaded when it is stored).
-        constexpr bool PF = LOAD_ITERS <= 4;
+        // registers would spill, so each stage is loaded when it is stored;
+        // likewise the v1 split kernel with scalar loads at D = 256, which
+        // spilled 5 VGPRs with the prefetch and needs 228 without it).
+        constexpr bool PF = LOAD_ITERS <= 4 && !(STREAM && VARIANT == 1 && LOADER == 0 && D == 256);
         f32x4 kr[LOAD_ITERS], vr[LOAD_ITERS];
         if (PF && nst > 0) {
             load_regs(Kh, k0, kr);
@@ -1014,7 +1017,15 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
         // split-KV layout fa_merge reads: O rows (unnormalised), m, l.
         const int qt = q0 / 16 + tile;
         if (qt >= p.nqt) return;
-        const float lt = row4_sum(l);
+        // v2/v3: l is this lane's part of the row sum and o unnormalised; v1
+        // keeps the row's full sum in l and o normalised by it (src/v1.rs:
+        // 313-385), so its partial is o * l -- fa_merge then weighs the
+        // normalised partials by l 2^(m - M) as it weighs v2's by 2^(m - M).
+        const float lt = VARIANT == 1 ? l : row4_sum(l);
+        if constexpr (VARIANT == 1) {
+#pragma unroll
+            for (int j = 0; j < NOB; ++j) o[j] *= lt;
+        }
         // key split: slot (bh, qt, split); stream split: the block slot
         // (workgroup + global block index) times the block's 16-row tiles
         const size_t pidx = p.stream_per > 0 ? (size_t)ysplit * TILES + tile
@@ -1061,7 +1072,7 @@ __device__ __forceinline__ StreamGeom stream_geom(const FaParams& p, int bq, int
     g.R = bq / sk_stage;
     g.nsf = (p.seq_k + sk_stage - 1) / sk_stage;
     g.bf = p.seq_k / bq;
-    g.causal = p.causal != 0;
+    g.causal = p.causal != 0 && !p.full_keys;   // v1: every block has all seq_k keys
     g.u_head = p.stream_head_units;
     return g;
 }
@@ -1161,7 +1172,6 @@ __device__ __forceinline__ void for_each_segment(const FaParams& p, F&& run) {
 // loop around them, or the partial stores, would take.
 template <int D, int VARIANT, int LOADER, bool STREAM>
 __device__ __forceinline__ void prefill_body(const FaParams& p) {
-    static_assert(!STREAM || VARIANT != 1, "v1 never splits its keys");
     for_each_segment<fa_prefill_rows(D), fa_prefill_stage_keys(D, VARIANT), STREAM, VARIANT == 3 && D == 128>(
         p, [&](const PrefillSeg& seg) {
             // (the opaque tid spills at D >= 512 and is not needed there)
@@ -1195,7 +1205,12 @@ __device__ __forceinline__ void prefill_body(const FaParams& p) {
 // 64 bytes per instruction (measured: 5.7-6.1 TB/s for that pattern against
 // 6.4-6.9 TB/s for whole rows).  No barriers: a wave only reads its own
 // slots, after s_waitcnt on its own DMA.
-template <int D, bool VEC, bool DBUF_REQ, typename E = float, bool KLDS = false>
+// V1: v1's recurrence (src/v1.rs:291-385) -- the accumulator kept normalised,
+// un-normalised by l * c before each block's PV and re-normalised by 1 / l
+// after it -- and no causal skip: every key of the split is visited and
+// masked, as v1 visits every tile.  The partial is un-normalised once at the
+// end (o * l), so the waves' merge and fa_merge weigh it like v2's.
+template <int D, bool VEC, bool DBUF_REQ, typename E = float, bool KLDS = false, bool V1 = false>
 __device__ __forceinline__ void decode_body(const FaParams& p) {
     constexpr bool DBUF = DBUF_REQ && D <= 128;
     static_assert(!KLDS || (DBUF && VEC && D >= 64 && std::is_same<E, float>::value),
@@ -1254,7 +1269,7 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
     const int kstep = 16;
     int kend = min(seq_k, kbeg + wave_len);
 #endif
-    if (causal) kend = min(kend, qlast + 1);
+    if (causal && !V1) kend = min(kend, qlast + 1);   // v2/v3: no key past the tile's last row
 
     // Q as the B operand: lane holds Q[qrow][16cc + 4lg + i] at qreg[4cc + i].
     float qreg[NQ];
@@ -1333,10 +1348,24 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
             ps += s[r];
         }
         const float corr = rescale_factor(m, m_use, c);
-        m = m_new;
-        l = corr * l + ps;
+        // v1: the row's full sum (its 4 lanes) every block; a block that
+        // changes nothing (no visible key, same max) skips the round trip
+        float inv = 1.0f;
+        if constexpr (V1) {
+            const float rs = row4_sum(ps);
+            const float l_new = corr * l + rs;
+            const bool moves = m_new != m || rs != 0.0f;
+            const float f = moves ? l * corr : 1.0f;
 #pragma unroll
-        for (int j = 0; j < NOB; ++j) o[j] *= corr;
+            for (int j = 0; j < NOB; ++j) o[j] *= f;
+            inv = !moves ? 1.0f : (l_new > 0.0f ? 1.0f / l_new : 0.0f);
+            l = l_new;
+        } else {
+            l = corr * l + ps;
+#pragma unroll
+            for (int j = 0; j < NOB; ++j) o[j] *= corr;
+        }
+        m = m_new;
         // O^T[dv][q] += V^T P^T: block (hh, j) row i <-> dv = 64hh + VW*i + j
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -1347,6 +1376,10 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
                 for (int j = 0; j < VW; ++j)
                     o[hh * VW + j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[j], s[r], o[hh * VW + j], 0, 0, 0);
             }
+        if constexpr (V1) {
+#pragma unroll
+            for (int j = 0; j < NOB; ++j) o[j] *= inv;
+        }
     };
 
     if constexpr (KLDS) {
@@ -1461,7 +1494,13 @@ __device__ __forceinline__ void decode_body(const FaParams& p) {
         }
     }
 
-    l = row4_sum(l);
+    if constexpr (V1) {
+        // l already holds the row's full sum; un-normalise the accumulator
+#pragma unroll
+        for (int j = 0; j < NOB; ++j) o[j] *= l;
+    } else {
+        l = row4_sum(l);
+    }
 
     // Merge the 4 waves through LDS: waves 1..3 write, wave 0 combines (with
     // LDS-staged K, into slot 0 once every wave has read its last block).
@@ -1586,7 +1625,7 @@ __device__ __forceinline__ void merge_body(const FaParams& p) {
         pstride = (size_t)(p.ks_rows / 16);
         pbase = ((size_t)first + (size_t)bh * p.nqb + blk) * pstride + (q % p.ks_rows) / 16;
     } else if (p.ks_rows > 0) {
-        const int kend = p.causal ? min(p.seq_k, (q / p.ks_rows + 1) * p.ks_rows) : p.seq_k;
+        const int kend = (p.causal && !p.full_keys) ? min(p.seq_k, (q / p.ks_rows + 1) * p.ks_rows) : p.seq_k;
         ns = min(ns, (kend + p.split_len - 1) / p.split_len);
     }
 
@@ -1826,7 +1865,8 @@ __device__ __forceinline__ void naive_pv_body(const NaiveParams& p) {
 // Named entry points for hipModuleGetFunction.
 // ---------------------------------------------------------------------------
 // fa_prefill_v{V}_d{D}_{L}: L = 0 scalar loads, 1 vector loads, 2 LDS DMA (v3);
-// fa_prefill_v{V}_d{D}_{L}s: the stream split (v2 / v3).
+// fa_prefill_v{V}_d{D}_{L}s: the split instantiation (stream split and key
+// split; v1 keeps its per-stage normalisation and visits every key).
 #define FA_PREFILL(D, VAR, LD)                                                                   \
     extern "C" __global__ void __launch_bounds__(64 * fa_prefill_waves(D), 8 / fa_prefill_waves(D))   \
         fa_prefill_v##VAR##_d##D##_##LD(FaParams p) {                                                \
@@ -1840,6 +1880,8 @@ __device__ __forceinline__ void naive_pv_body(const NaiveParams& p) {
 #define FA_PREFILL_ALL(D)  \
     FA_PREFILL(D, 1, 0)    \
     FA_PREFILL(D, 1, 1)    \
+    FA_PREFILL_S(D, 1, 0)  \
+    FA_PREFILL_S(D, 1, 1)  \
     FA_PREFILL(D, 2, 0)    \
     FA_PREFILL(D, 2, 1)    \
     FA_PREFILL(D, 3, 0)    \
@@ -1863,6 +1905,8 @@ FA_PREFILL(1024, 2, 0)
 FA_PREFILL(1024, 2, 1)
 FA_PREFILL(1024, 3, 0)
 FA_PREFILL(1024, 3, 1)
+FA_PREFILL_S(1024, 1, 0)
+FA_PREFILL_S(1024, 1, 1)
 FA_PREFILL_S(1024, 2, 0)
 FA_PREFILL_S(1024, 2, 1)
 FA_PREFILL_S(1024, 3, 0)
@@ -1893,6 +1937,27 @@ FA_DECODE(256, 0, 1, 1)
     }
 FA_DECODE_KLDS(64)
 FA_DECODE_KLDS(128)
+// fa_decode_v1_d{D}_{L}: v1's per-block normalisation, every key visited.
+// D = 128 with scalar loads re-issues each operand's loads once consumed (no
+// register double buffer): with it the kernel spilled 32 VGPRs.
+#define FA_DECODE_V1(D, VEC, DBUF, OCC)                                                          \
+    extern "C" __global__ void __launch_bounds__(256, OCC) fa_decode_v1_d##D##_##VEC(FaParams p) { \
+        decode_body<D, VEC != 0, DBUF, float, false, true>(p);                                   \
+    }
+FA_DECODE_V1(32, 1, true, 4)
+FA_DECODE_V1(32, 0, true, 4)
+FA_DECODE_V1(64, 1, true, 3)
+FA_DECODE_V1(64, 0, true, 3)
+FA_DECODE_V1(128, 1, true, 2)
+FA_DECODE_V1(128, 0, false, 2)
+FA_DECODE_V1(256, 1, false, 1)
+FA_DECODE_V1(256, 0, false, 1)
+#define FA_DECODE_KLDS_V1(D)                                                                      \
+    extern "C" __global__ void __launch_bounds__(256, 2) fa_decode_v1_d##D##_2(FaParams p) {      \
+        decode_body<D, true, true, float, true, true>(p);                                         \
+    }
+FA_DECODE_KLDS_V1(64)
+FA_DECODE_KLDS_V1(128)
 
 // fa_decode_{bf16,f16}_d{D}_{VEC}: 16-bit Q/K/V widened to f32 as loaded.
 #define FA_DECODE_LP(D, TN, T, VEC, OCC1, OCC2)                                                   \
@@ -1918,7 +1983,13 @@ FA_DECODE_LP_ALL(f16, _Float16)
     extern "C" __global__ void __launch_bounds__(256, 2) fa_decode_rows_d##D##_q##RQ(FaParams p) { \
         decode_rows_body<D, RQ>(p);                                                              \
     }
-#define FA_DECODE_ROWS_ALL(D) FA_DECODE_ROWS(D, 1) FA_DECODE_ROWS(D, 2) FA_DECODE_ROWS(D, 4)
+// fa_decode_rows_v1_d{D}_q{RQ}: the same with v1's per-block normalisation
+#define FA_DECODE_ROWS_V1(D, RQ)                                                                 \
+    extern "C" __global__ void __launch_bounds__(256, 2) fa_decode_rows_v1_d##D##_q##RQ(FaParams p) { \
+        decode_rows_body<D, RQ, float, true>(p);                                                 \
+    }
+#define FA_DECODE_ROWS_ALL(D) FA_DECODE_ROWS(D, 1) FA_DECODE_ROWS(D, 2) FA_DECODE_ROWS(D, 4) \
+    FA_DECODE_ROWS_V1(D, 1) FA_DECODE_ROWS_V1(D, 2) FA_DECODE_ROWS_V1(D, 4)
 FA_DECODE_ROWS_ALL(32)
 FA_DECODE_ROWS_ALL(64)
 FA_DECODE_ROWS_ALL(128)

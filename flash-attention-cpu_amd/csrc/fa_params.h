@@ -32,6 +32,9 @@ typedef struct FaParams {
                          // block); 0 = plain longest-first order
     int two_blocks;      // f32 v3 prefill, d_head 128: each workgroup runs query blocks
                          // nqb-1-r and r of one (batch, head); nqb even, grid = bh * nqb / 2
+    int full_keys;       // v1: every query block visits all seq_k keys, causal or not (no
+                         // causal skip), so the key split, the stream split and fa_merge
+                         // count each block's keys as the whole key range
     long long stream_per;         // stream split (v2/v3 prefill): key stages per workgroup; 0 = off
     long long stream_head_units;  // stream split: key stages of one slice (all its query blocks)
 } FaParams;

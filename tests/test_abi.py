@@ -8,7 +8,7 @@
 * without a visible device every compute entry point fails loudly with
   FA_ERR_NO_DEVICE (no CPU fallback exists);
 * launch planning (fa_describe_launch): kernel choice per d_head, load path,
-  split-KV for short queries, v1 never split, unsupported d_head.
+  split-KV for short queries, v1's own split instantiations, unsupported d_head.
 """
 from __future__ import annotations
 
@@ -217,11 +217,16 @@ def test_planning_split_kv():
     assert describe(2, 1, 32, 1, 32768, 128, False, dtype=fa.DTYPE_BF16).startswith("fa_decode_rows_bf16_d128_q1")
     assert describe(2, 1, 32, 1, 32768, 256, False, dtype=fa.DTYPE_F16).startswith("fa_decode_rows_f16_d256_q1")
     assert describe(2, 1, 32, 2, 32768, 128, False, dtype=fa.DTYPE_BF16).startswith("fa_prefill_lp_bf16")
-    with pytest.raises(fa.FaError) as e:
-        describe(1, 1, 4, 1, 1000, 64, False, fa.PATH_SPLITKV_ROWS)   # v1 never splits
-    assert e.value.status == fa.FA_ERR_INVALID_ARG
+    # v1 takes split-KV too, on its own instantiations (per-block normalisation, no causal skip)
+    assert describe(1, 1, 4, 1, 1000, 64, False, fa.PATH_SPLITKV_ROWS).startswith("fa_decode_rows_v1_d64_q1 grid=12x1x1")
     assert "fa_decode" in describe(3, 1, 32, 16, 32768, 128, False)
-    assert "fa_decode" not in describe(1, 1, 32, 16, 32768, 128, False)   # v1 keeps FA-1's loop
+    assert describe(1, 1, 32, 16, 32768, 128, False).startswith("fa_decode_v1_d128_2 grid=256x1x1")      # config 4b
+    s = describe(1, 1, 32, 1, 32768, 128, False)                                                          # config 4a
+    assert s.startswith("fa_decode_rows_v1_d128_q1 grid=512x1x1") and "fa_merge_d128 grid=8x1x1" in s
+    assert describe(1, 1, 1, 256, 256, 64, False) == "fa_decode_v1_d64_2 grid=16x1x1 block=256"          # config 1
+    assert describe(1, 1, 8, 5, 9000, 128, True, fa.PATH_SPLITKV, 0).startswith("fa_decode_v1_d128_2 ")
+    assert describe(1, 1, 8, 5, 9000, 200, True, fa.PATH_SPLITKV, 0).startswith("fa_decode_v1_d256_1 ")
+    assert describe(1, 1, 8, 5, 9000, 126, True, fa.PATH_SPLITKV, 0).startswith("fa_decode_v1_d128_0 ")
     assert "fa_decode" in describe(2, 1, 32, 16, 200, 128, False)         # short keys too
     assert describe(2, 1, 512, 1, 64, 128, False) == "fa_decode_rows_d128_q1 grid=512x1x1 block=256"
     assert "fa_decode" not in describe(2, 1, 32, 33, 200, 128, False)     # three tiles, short keys: prefill
@@ -297,7 +302,14 @@ def test_planning_key_split_prefill():
     # compact grid: split y of every 128-row block whose causal key end passes y * split_len
     wgs = 16 * sum(1 for y in range(nks) for qb in range(8) if min(1000, 128 * (qb + 1)) > y * split_len)
     assert f"grid={wgs}x1x1" in s
-    assert "fa_merge" not in describe(1, 1, 16, 1000, 1000, 256, True)     # v1 never splits
+    # v1 (config 5c): every block visits all 1000 keys = 32 stages of 32; two splits of 16 stages
+    s = describe(1, 1, 16, 1000, 1000, 256, True)
+    assert s.startswith("fa_prefill_v1_d256_1s grid=256x1x1 block=512; fa_merge_d256 grid=4000x1x1 ")
+    assert "splits=2 split_len=512" in s and "stream_per" not in s
+    s = describe(1, 1, 16, 1000, 1000, 256, True, fa.PATH_PREFILL, 3)   # forced: all 8 blocks in every split
+    assert s.startswith("fa_prefill_v1_d256_1s grid=384x1x1") and "splits=3 split_len=352" in s
+    s = describe(1, 1, 16, 1000, 1000, 256, True, fa.PATH_STREAM)        # 16 x 8 x 32 stages in 256 runs of 16
+    assert s.startswith("fa_prefill_v1_d256_1s grid=256x1x1") and "stream_per=16" in s
     assert "fa_merge" not in describe(3, 1, 32, 2048, 2048, 128, True)    # full grid
     s = describe(2, 1, 1, 300, 700, 64, False, fa.PATH_PREFILL, 3)   # 11 stages of 64 keys -> 4 per split
     assert s.startswith("fa_prefill_v2_d64_1s grid=9x1x1") and "splits=3 split_len=256" in s
@@ -329,9 +341,7 @@ def test_planning_errors():
         with pytest.raises(fa.FaError) as e:
             describe(2, 1, 1, 10, 10, 1025, False, **kw)
         assert e.value.status == fa.FA_ERR_UNSUPPORTED, kw
-    with pytest.raises(fa.FaError) as e:
-        describe(1, 1, 1, 10, 1000, 64, False, fa.PATH_SPLITKV)
-    assert e.value.status == fa.FA_ERR_INVALID_ARG
+    assert describe(1, 1, 1, 10, 1000, 64, False, fa.PATH_SPLITKV).startswith("fa_decode_v1_d64_2 grid=3x1x1")
     with pytest.raises(fa.FaError) as e:
         describe(4, 1, 1, 10, 10, 64, False)
     assert e.value.status == fa.FA_ERR_INVALID_ARG
@@ -390,7 +400,7 @@ def test_planning_16bit_inputs():
     assert describe(2, 1, 1, 4, 512, 64, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_F16).startswith("fa_decode_f16_d64_1")
     assert describe(3, 1, 1, 4, 512, 62, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_F16).startswith("fa_decode_f16_d64_0")
     with pytest.raises(fa.FaError) as e:
-        describe(1, 1, 1, 4, 512, 64, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_BF16)   # v1 never splits
+        describe(1, 1, 1, 4, 512, 64, False, fa.PATH_SPLITKV, dtype=fa.DTYPE_BF16)   # no 16-bit v1 kernels
     assert e.value.status == fa.FA_ERR_INVALID_ARG
     with pytest.raises(fa.FaError) as e:
         describe(3, 1, 1, 4, 512, 64, False, dtype=7)

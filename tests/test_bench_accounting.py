@@ -73,9 +73,7 @@ def test_traffic_lookup_requires_matching_kernel_sources(tmp_path):
 
 def test_bench_rows_have_distinct_launch_keys():
     """profiles/ key kernel figures by (kernel, launch size): two bench rows
-    whose launches share a key would have their counters averaged.  The one
-    shared key is v1 of configs 4a and 4b, the same kernel over the same 32
-    prefill blocks and the same K / V bytes."""
+    whose launches share a key would have their counters averaged."""
     import flash_attention_amd as fa
     use = {}
     for (name, bh, sq, sk, d, causal, *_rest) in bench.CONFIGS:
@@ -87,7 +85,7 @@ def test_bench_rows_have_distinct_launch_keys():
                 if "grid=" in part:
                     use.setdefault((part.split()[0], bench.grid_threads(part)), set()).add(name)
     shared = {k: v for k, v in use.items() if len(v) > 1}
-    assert shared == {("fa_prefill_v1_d128_1", 16384): {"config4a", "config4b"}}, shared
+    assert shared == {}, shared
 
 
 

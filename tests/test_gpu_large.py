@@ -128,7 +128,7 @@ def test_decode_k_and_v_past_2_31_elements():
         assert max_abs_diff(want, v_host.reshape(sk, D)[own[:sq]].ravel()) < 1e-3
         buf = torch.full((sq * D + 2 * GUARD,), 12.5, device=dev)
         out = buf[GUARD:GUARD + sq * D]
-        for variant in (2, 3):
+        for variant in (1, 2, 3):
             plan = fa.describe_launch(variant, 1, 1, sq, sk, D, False)
             print(f"[case] large decode v{variant} {sq}x{sk} d={D}: {plan}", flush=True)
             out.fill_(-3.0)

@@ -151,7 +151,7 @@ def test_wide_heads_multiblock_and_key_split(d):
             assert_parity(outs[variant], want, f"v{variant} {bh},{sq},{sk},{d},{causal}")
         assert_parity(outs[1], outs[2], "v1 vs v2")
         assert_parity(outs[3], outs[2], "v3 vs v2")
-        for variant in (2, 3):
+        for variant in ALL_VARIANTS:
             for splits in (2, 3, 5):
                 plan = fa.describe_launch(variant, 1, bh, sq, sk, d, causal, fa.PATH_PREFILL, splits)
                 out = _device_run(variant, q, k, v, bh, sq, sk, d, causal, fa.PATH_PREFILL, splits, guard=64)
@@ -302,12 +302,16 @@ def test_differential_fuzz_split_paths():
         if sq <= 4 and d % 4 == 0:
             paths.append((fa.PATH_SPLITKV_ROWS, 0))
         for path, splits in paths:
-            tag = f"it={it} path={path} ({bh},{sq},{sk},{d},{causal}) mag={mag}"
-            print("[case]", tag, flush=True)
-            out = _device_run(3, q, k, v, bh, sq, sk, d, causal, path, splits, guard=64)
-            assert np.array_equal(np.isfinite(out), np.isfinite(want)), tag
-            tol = 1e-1 * (np.maximum(np.abs(out), np.abs(want)) + 1.0)
-            assert np.all(np.abs(out - want) < tol), tag
+            outs = {}
+            for variant in (1, 3):   # v1's split kernels (per-block normalisation) and v3's
+                tag = f"it={it} v{variant} path={path} ({bh},{sq},{sk},{d},{causal}) mag={mag}"
+                print("[case]", tag, flush=True)
+                out = outs[variant] = _device_run(variant, q, k, v, bh, sq, sk, d, causal, path, splits, guard=64)
+                assert np.array_equal(np.isfinite(out), np.isfinite(want)), tag
+                tol = 1e-1 * (np.maximum(np.abs(out), np.abs(want)) + 1.0)
+                assert np.all(np.abs(out - want) < tol), tag
+            if mag == 1.0:
+                assert_parity(outs[1], outs[3], f"it={it} v1 vs v3 path={path}")
 
 
 def test_differential_fuzz_new_paths():
@@ -337,7 +341,7 @@ def test_differential_fuzz_new_paths():
         k = (rng.uniform(-1, 1, bh * sk * d) * mag).astype(np.float32)
         v = (rng.uniform(-1, 1, bh * sk * d)).astype(np.float32)
         want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
-        for variant in (2, 3):
+        for variant in ALL_VARIANTS:
             plan = fa.describe_launch(variant, 1, bh, sq, sk, d, causal, path, splits)
             tag = f"it={it} v{variant} ({bh},{sq},{sk},{d},{causal}) mag={mag}: {plan}"
             print("[case]", tag, flush=True)
@@ -365,10 +369,15 @@ def test_config1_single_head_256():
     sq = sk = 256
     d = 64
     q, k, v = _qkv(1, sq, sk, d)
+    want = cpu_v2(q, k, v, 1, sq, sk, d, False)
     out = np.zeros(sq * d, dtype=np.float32)
     fa.flash_attention(q, k, v, sq, sk, d, fa.FlashAttentionConfig(), out)
-    assert_parity(out, cpu_v2(q, k, v, 1, sq, sk, d, False), "config 1")
+    assert_parity(out, want, "config 1")
     assert max_abs_diff(out, attention_f64(q, k, v, sq, sk, d, False)) < 2e-5
+    for variant in ALL_VARIANTS:
+        out = np.zeros(sq * d, dtype=np.float32)
+        fa.VARIANTS[variant](q, k, v, sq, sk, d, fa.FlashAttentionConfig(), out)
+        assert_parity(out, want, f"config 1 v{variant}")
 
 
 @pytest.mark.parametrize("variant", ALL_VARIANTS)
@@ -466,7 +475,7 @@ def test_split_kv_matches_oracle_and_prefill():
         pre = _device_run(2, q, k, v, bh, sq, sk, d, causal, fa.PATH_PREFILL, guard=64)
         assert_parity(pre, want, f"prefill {bh},{sq},{sk},{d},{causal}")
         for splits in (0, 1, 2, 3, 7):
-            for variant in (2, 3):
+            for variant in ALL_VARIANTS:
                 got = _device_run(variant, q, k, v, bh, sq, sk, d, causal, fa.PATH_SPLITKV, splits, guard=64)
                 assert_parity(got, want, f"split-kv v{variant} splits={splits} {bh},{sq},{sk},{d},{causal}")
 
@@ -488,7 +497,7 @@ def test_row_streaming_decode_matches_oracle():
         v = rng.standard_normal(bh * sk * d, dtype=np.float32)
         want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
         for splits in (0, 1, 2, 3, 7, 40):
-            for variant in (2, 3):
+            for variant in ALL_VARIANTS:
                 tag = f"rows v{variant} splits={splits} {bh},{sq},{sk},{d},{causal},sigma={sigma}"
                 print("[case]", tag, flush=True)
                 got = _device_run(variant, q, k, v, bh, sq, sk, d, causal, fa.PATH_SPLITKV_ROWS, splits, guard=64)
@@ -534,7 +543,7 @@ def test_single_split_decode_writes_rows_directly():
         k = rng.standard_normal(bh * sk * d, dtype=np.float32)
         v = rng.standard_normal(bh * sk * d, dtype=np.float32)
         want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
-        for variant in (2, 3):
+        for variant in ALL_VARIANTS:
             tag = f"v{variant} {plan} ({bh},{sq},{sk},{d},{causal})"
             print("[case]", tag, flush=True)
             assert_parity(_device_run(variant, q, k, v, bh, sq, sk, d, causal, path, 1, guard=64), want, tag)
@@ -558,7 +567,7 @@ def test_batched_decode_steps_take_split_kv():
         k = rng.standard_normal(bh * sk * d, dtype=np.float32)
         v = rng.standard_normal(bh * sk * d, dtype=np.float32)
         want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
-        for variant in (2, 3):
+        for variant in ALL_VARIANTS:
             tag = f"v{variant} {plan}"
             print("[case]", tag, flush=True)
             assert_parity(_device_run(variant, q, k, v, bh, sq, sk, d, causal, guard=64), want, tag)
@@ -578,14 +587,14 @@ def test_small_prefill_on_split_kv_tiles_matches_oracle():
         k = rng.standard_normal(bh * sk * d, dtype=np.float32)
         v = rng.standard_normal(bh * sk * d, dtype=np.float32)
         want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
-        for variant in (2, 3):
+        for variant in ALL_VARIANTS:
             tag = f"small prefill v{variant} {bh},{sq},{sk},{d},{causal}"
             print("[case]", tag, plan, flush=True)
             assert_parity(_device_run(variant, q, k, v, bh, sq, sk, d, causal, guard=64), want, tag)
 
 
 def test_key_split_prefill_matches_oracle():
-    """v2/v3 query-block kernel with each block's keys divided over several
+    """v1/v2/v3 query-block kernels with each block's keys divided over several
     workgroups and the partials merged (forced here; chosen automatically on
     grids smaller than the GPU)."""
     rng = np.random.default_rng(78)
@@ -597,13 +606,13 @@ def test_key_split_prefill_matches_oracle():
         v = rng.standard_normal(bh * sk * d, dtype=np.float32)
         want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
         for splits in (2, 3, 5, 16):
-            for variant in (2, 3):
+            for variant in ALL_VARIANTS:
                 tag = f"key-split v{variant} splits={splits} {bh},{sq},{sk},{d},{causal}"
                 print("[case]", tag, flush=True)
                 got = _device_run(variant, q, k, v, bh, sq, sk, d, causal, fa.PATH_PREFILL, splits, guard=64)
                 assert_parity(got, want, tag)
         # automatic choice (small grid) and its determinism
-        for variant in (2, 3):
+        for variant in ALL_VARIANTS:
             a = _device_run(variant, q, k, v, bh, sq, sk, d, causal, guard=64)
             b = _device_run(variant, q, k, v, bh, sq, sk, d, causal, guard=64)
             assert np.array_equal(a, b)
@@ -611,7 +620,7 @@ def test_key_split_prefill_matches_oracle():
 
 
 def test_stream_split_prefill_matches_oracle():
-    """v2/v3 query-block kernel with the stream split: the key stages of all
+    """v1/v2/v3 query-block kernels with the stream split: the key stages of all
     (slice, query block) pairs cut into equal runs, one per workgroup, runs
     crossing block and slice boundaries, shared blocks merged (forced here
     with several workgroup counts; chosen automatically for small causal
@@ -627,16 +636,15 @@ def test_stream_split_prefill_matches_oracle():
         v = rng.standard_normal(bh * sk * d, dtype=np.float32)
         want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
         for splits in (0, 1, 3, 7, 64):
-            for variant in (2, 3):
+            for variant in ALL_VARIANTS:
                 plan = fa.describe_launch(variant, 1, bh, sq, sk, d, causal, fa.PATH_STREAM, splits)
                 tag = f"stream v{variant} workgroups={splits} {bh},{sq},{sk},{d},{causal}: {plan}"
                 print("[case]", tag, flush=True)
                 assert "stream_per=" in plan, tag
                 got = _device_run(variant, q, k, v, bh, sq, sk, d, causal, fa.PATH_STREAM, splits, guard=64)
                 assert_parity(got, want, tag)
-    with pytest.raises(fa.FaError) as e:
-        fa.describe_launch(1, 1, 16, 1000, 1000, 256, True, fa.PATH_STREAM)
-    assert e.value.status == fa.FA_ERR_INVALID_ARG   # v1 never splits its keys
+    # v1 splits with every block visiting all keys (no causal skip)
+    assert "stream_per=16" in fa.describe_launch(1, 1, 16, 1000, 1000, 256, True, fa.PATH_STREAM)
     assert "stream_per=18" in fa.describe_launch(3, 1, 16, 1000, 1000, 256, True)   # config 5c: automatic
 
 

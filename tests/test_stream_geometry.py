@@ -149,17 +149,19 @@ def _key_split_cases():
     return cases
 
 
+@pytest.mark.parametrize("variant", (1, 3))
 @pytest.mark.parametrize("case", _key_split_cases())
-def test_key_split_writers_match_merged_splits(case):
+def test_key_split_writers_match_merged_splits(case, variant):
     """map_block_split's compact grid: split y holds every block whose key
-    range reaches y * split_len (causal: blocks qb >= floor(y * split_len /
-    rows)).  For each block, the splits listed (the partials written) must be
-    the splits fa_merge reads: the first min(num_splits, ceil(block key end /
-    split_len))."""
+    range reaches y * split_len (causal v2/v3: blocks qb >= floor(y *
+    split_len / rows); v1 visits every key, so every block).  For each block,
+    the splits listed (the partials written) must be the splits fa_merge
+    reads: the first min(num_splits, ceil(block key end / split_len))."""
     import flash_attention_amd as fa
     bh, sq, sk, d, causal, splits = case
+    skip_future = causal and variant != 1   # v1: no causal skip (src/v1.rs:209-216)
     try:
-        s = fa.describe_launch(3, 1, bh, sq, sk, d, causal, fa.PATH_PREFILL, splits)
+        s = fa.describe_launch(variant, 1, bh, sq, sk, d, causal, fa.PATH_PREFILL, splits)
     except fa.FaError:
         pytest.skip("plan refused")
     if "split_len=" not in s or "stream_per" in s:
@@ -172,11 +174,30 @@ def test_key_split_writers_match_merged_splits(case):
     writers = [0] * nqb
     listed = 0
     for y in range(nks):
-        cnt = nqb - (y * split_len) // rows if causal else nqb
+        cnt = nqb - (y * split_len) // rows if skip_future else nqb
         for rank in range(max(cnt, 0)):
             writers[nqb - 1 - rank if causal else rank] += 1
         listed += max(cnt, 0) * bh
     assert listed == grid, s
     for qb in range(nqb):
-        kend = min(sk, (qb + 1) * rows) if causal else sk
+        kend = min(sk, (qb + 1) * rows) if skip_future else sk
         assert writers[qb] == min(nks, -(-kend // split_len)), (qb, s)
+
+
+@pytest.mark.parametrize("case", CASES[:6] + _random_cases(20, 7))
+def test_v1_stream_split_counts_every_key(case):
+    """v1 visits every key of every block, causal or not: its stream split
+    is planned on the non-causal unit geometry (each block nsf stages), which
+    test_stream_split_covers_every_unit_once checks; here the host's plan for
+    v1 must match that geometry's run length and workgroup count."""
+    import flash_attention_amd as fa
+    bh, sq, sk, bq, skk, causal, want = case
+    d = {64: 64, 32: 256}.get(skk) if bq == 128 else None
+    if d is None:
+        pytest.skip("v1 stages of 128-row blocks: 64 keys at d <= 128, 32 at d = 256")
+    try:
+        s = fa.describe_launch(1, 1, bh, sq, sk, d, causal, fa.PATH_STREAM, want)
+    except fa.FaError:
+        pytest.skip("plan refused")
+    g, nqb, u_head, per, wgs, segs, slots = plan(bh, sq, sk, bq, skk, False, want)
+    assert f"stream_per={per}" in s and f"grid={wgs}x1x1" in s, (s, per, wgs)
