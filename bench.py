@@ -10,9 +10,9 @@ the launch stream) against the FP32-MFMA peak, and ``roofline.traffic`` is
 the kernel's measured HBM bytes per launch (rocprofv3 counters, reported only
 while the kernel sources match the ones profiled).
 
-Every other configuration (1, 3, 4a, 4b, 5, 5c; v1/v2/v3), and three shapes
-beyond BASELINE.json (wide heads of d_head 512 and 1024, and a batched decode
-step of 768 slices), is timed the same way into
+Every other configuration (1, 3, 4a, 4b, 5, 5c; v1/v2/v3), and four shapes
+beyond BASELINE.json (wide heads of d_head 512, 1024 and 2048, and a batched
+decode step of 768 slices), is timed the same way into
 ``extra.configs`` -- TFLOP/s and % of the FP32-MFMA peak for
 prefill shapes, GB/s and % of 8 TB/s for decode shapes -- next to a CPU
 baseline on the same inputs: the oracle's v2 (oracle/, a C restatement of the
@@ -62,6 +62,7 @@ CONFIGS = [
     # flash kernels (the crate's flash path takes any d_head)
     ("wide_d512", 16, 2048, 2048, 512, True, 1.0, False, "prefill"),
     ("wide_d1024", 8, 2048, 2048, 1024, True, 1.0, False, "prefill"),
+    ("wide_d2048", 4, 2048, 2048, 2048, True, 1.0, False, "prefill"),
     # batched decode step: 768 (sequence, head) slices of one query over
     # 2048 keys, the split-KV row kernel whatever the grid size (launch
     # sizes of its own for every variant: profiles key kernels by name and

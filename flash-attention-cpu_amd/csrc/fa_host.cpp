@@ -38,7 +38,7 @@
 namespace {
 
 constexpr int kMaxDevices = 64;
-constexpr int kMaxD = 1024;         // widest head of the f32 flash kernels
+constexpr int kMaxD = 2048;         // widest head of the f32 flash kernels
 constexpr int kMaxDNarrow = 256;    // 16-bit kernels and the split-KV decoders
 constexpr int kDecodeRows = 16;     // query rows per split-KV wave
 constexpr int kDecodeWaves = 4;     // waves per split-KV workgroup
@@ -276,7 +276,8 @@ int pad_d(size_t d) {
     if (d <= 128) return 128;
     if (d <= 256) return 256;
     if (d <= 512) return 512;
-    return 1024;
+    if (d <= 1024) return 1024;
+    return 2048;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -388,9 +389,10 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
             std::snprintf(buf, sizeof(buf), "fa_prefill_lp_%s_d%d_%d_t%d", dtype == FA_DTYPE_BF16 ? "bf16" : "f16",
                           D, vec ? 2 : 0, lp_tiles);
         } else {
-            // 0: scalar loads (any d), 1: 128-bit loads, 2: global->LDS DMA (v3
-            // with two LDS stages; D = 1024 holds one)
-            const int loader = vec ? (fa_prefill_nbuf(D, variant) == 2 ? 2 : 1) : 0;
+            // 0: scalar loads (any d), 1: 128-bit loads, 2: global->LDS DMA (v3:
+            // two LDS stages, or at D = 1024 alternating K and V buffers; not
+            // at D = 2048)
+            const int loader = vec ? (fa_prefill_dma(D, variant) ? 2 : 1) : 0;
             std::snprintf(buf, sizeof(buf), "fa_prefill_v%d_d%d_%d", variant, D, loader);
         }
         plan->first.name = buf;
@@ -710,7 +712,7 @@ int stream_workspace(int dev, hipStream_t stream, size_t bytes, void** out) {
 int run_naive_device(hipStream_t stream, const float* q, const float* k, const float* v, size_t bh, size_t sq,
                      size_t sk, size_t d, int causal, int precision, float* out, float scale);
 
-// Heads wider than the flash kernels' 1024 columns (the crate takes any
+// Heads wider than the flash kernels' 2048 columns (the crate takes any
 // d_head): f32 inputs on the automatic path run the naive kernels over a
 // materialised score matrix (src/naive.rs:14-75, in f32 with the same
 // 1/sqrt(d) or explicit scale), in head chunks capped by free device
@@ -1102,7 +1104,7 @@ const char* fa_status_string(int status) {
         case FA_ERR_V_SHAPE: return "v shape mismatch";
         case FA_ERR_OUT_SHAPE: return "out shape mismatch";
         case FA_ERR_INVALID_ARG: return "invalid argument";
-        case FA_ERR_UNSUPPORTED: return "unsupported shape (d_head > 256 with 16-bit inputs or split-KV, d_head > 1024 off the automatic f32 path, or size beyond 32-bit indexing)";
+        case FA_ERR_UNSUPPORTED: return "unsupported shape (d_head > 256 with 16-bit inputs or split-KV, d_head > 2048 off the automatic f32 path, or size beyond 32-bit indexing)";
         case FA_ERR_NO_DEVICE: return "no HIP device available";
         case FA_ERR_MODULE: return "cannot load the gfx950 code object (fa_kernels.hsaco / FA_HIP_MODULE)";
         case FA_ERR_ALLOC: return "device allocation failed";
@@ -1305,7 +1307,7 @@ int fa_describe_launch(int variant, size_t batch, size_t heads, size_t sq, size_
         if (d > (size_t)kMaxD) {
             rc = wide_head_status(variant, opts);
             if (rc == FA_OK)
-                text = "fa_naive_scores_f32; fa_naive_softmax_f32; fa_naive_pv_f32 (d_head > 1024: materialised scores)";
+                text = "fa_naive_scores_f32; fa_naive_softmax_f32; fa_naive_pv_f32 (d_head > 2048: materialised scores)";
         } else {
             rc = make_plan(variant, dummy, dummy, dummy, dummy, bh, sq, sk, d, causal, opts, num_cus, &plan);
         }

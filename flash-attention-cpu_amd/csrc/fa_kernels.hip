@@ -322,15 +322,23 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
     constexpr bool DMA = (LOADER == 2);
     constexpr int NBUF = fa_prefill_nbuf(D, VARIANT);
     constexpr bool PIPE = NBUF == 2;          // v3's double-buffered schedule
+    // v3 where one K + V stage is all the LDS holds (D = 1024): the K and V
+    // buffers alternate (V of a stage streams in under its QK^T, K of the
+    // next under its softmax + PV)
+    constexpr bool KVPP = VARIANT == 3 && !PIPE && DMA;
     static_assert(NVR * VW == NOB, "V read layout");
-    static_assert(!DMA || PIPE, "LDS DMA needs the double-buffered pipeline");
+    static_assert(!DMA || PIPE || KVPP, "LDS DMA needs one of v3's overlapped schedules");
     static_assert((SK * CPR) % NT == 0, "stage load must split evenly");
     static_assert(BQ == 16 * TILES && CG * DW == D, "column groups");
 
+    // D = 2048: one 16-key stage of K or V takes 129 KiB, so K and V take
+    // turns in one buffer (Kb0, sized for the longer V rows).
+    constexpr bool KV1 = D > 1024;
+    static_assert(!KV1 || (!PIPE && !DMA), "the shared K / V buffer is register-filled, one stage");
     // Separate arrays so the compiler can tell a DMA in flight into one
     // buffer from LDS reads of another (no needless vmcnt waits).
-    __shared__ __attribute__((aligned(16))) float Kb0[KTILE];
-    __shared__ __attribute__((aligned(16))) float Vb0[VTILE];
+    __shared__ __attribute__((aligned(16))) float Kb0[KV1 ? (KTILE > VTILE ? KTILE : VTILE) : KTILE];
+    __shared__ __attribute__((aligned(16))) float Vb0[KV1 ? 4 : VTILE];
     __shared__ __attribute__((aligned(16))) float Kb1[NBUF > 1 ? KTILE : 4];
     __shared__ __attribute__((aligned(16))) float Vb1[NBUF > 1 ? VTILE : 4];
     // Column groups: per-wave partial scores, one slot per wave (two in the
@@ -451,7 +459,7 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
     // wave (s_memtime): with every wave filling, each spent 0.9-1.3k cycles
     // per stage issuing its DMA right after the barrier, with neither wave of
     // a SIMD issuing MFMAs meanwhile.
-    constexpr int FW = (DMA && FA_FILL_HALF) ? NW / 2 : NW;
+    constexpr int FW = (DMA && FA_FILL_HALF && PIPE) ? NW / 2 : NW;
     const int fwave = wave - (NW - FW);   // index among the filling waves; < 0: does not fill
     auto dma_geometry = [&](auto ld, int* voff) {
         constexpr int RCH = decltype(ld)::value / 4;   // chunks per padded row
@@ -969,6 +977,84 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
         };
         if (early) run_steps(std::true_type{});
         else run_steps(std::false_type{});
+    } else if constexpr (KVPP) {
+        // One K buffer and one V buffer (src/v3.rs:445-483's overlap of the
+        // next tile's loads with the current tile's work, with the buffers
+        // taking turns): V(st) streams in by DMA while QK^T(st) reads K(st),
+        // and K(st + 1) while softmax + PV(st) read V(st).  Two barriers per
+        // stage, each after the DMA it waits for has had a compute phase to
+        // land; the first also publishes the column groups' partial scores.
+        if (nst > 0) fill_stage(KL, Kh, k0, Kb0);
+        wait_vmcnt<0>();
+        __syncthreads();
+        for (int st = 0; st < nst; ++st) {
+            const int kbase = k0 + st * SK;
+            fill_stage(VL, Vh, kbase, Vb0);   // V buffer free: the last PV ended before the barrier
+            const bool act = stage_active(st);
+            f32x4 s[KB];
+            if (act) {
+                qk_preload(Kb0);
+                qk_stage(Kb0, s);
+                xs_put(s, 0);
+            }
+            wait_vmcnt<0>();
+            __syncthreads();   // V(st) resident, K buffer free, partial scores visible
+            if (st + 1 < nst) fill_stage(KL, Kh, kbase + SK, Kb0);
+            if (act) {
+                xs_sum(s, 0);
+                mask_stage(s, kbase);
+                softmax_part(s);
+                pv_preload(Vb0);
+                pv_part(s, Vb0, no_hook);
+            }
+            wait_vmcnt<0>();
+            __syncthreads();   // K(st + 1) resident, V buffer and score slots free
+        }
+    } else if constexpr (KV1) {
+        // K and V of a stage in turn through the one buffer, each filled
+        // through registers in two halves (a whole stage is 64 VGPRs per
+        // lane): K, QK^T into the score slots, V, the softmax, PV.  Four
+        // barriers per stage; the softmax runs while other waves store V.
+        constexpr int HALF = LOAD_ITERS / 2;
+        static_assert(LOAD_ITERS % 2 == 0, "stage fill in halves");
+        auto fill_halves = [&](auto ld, const float* __restrict__ src, int kbase) {
+            constexpr int LD = decltype(ld)::value;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                f32x4 rg[HALF];
+#pragma unroll
+                for (int it = 0; it < HALF; ++it) {
+                    const int idx = tid + (h * HALF + it) * NT;
+                    rg[it] = load4<LOADER != 0>(src, kbase + idx / CPR, seq_k, 4 * (idx % CPR), d);
+                }
+#pragma unroll
+                for (int it = 0; it < HALF; ++it) {
+                    const int idx = tid + (h * HALF + it) * NT;
+                    *reinterpret_cast<f32x4*>(Kb0 + lds_off<LD>(idx / CPR, idx % CPR)) = rg[it];
+                }
+            }
+        };
+        for (int st = 0; st < nst; ++st) {
+            const int kbase = k0 + st * SK;
+            fill_halves(KL, Kh, kbase);
+            __syncthreads();   // K(st) resident
+            const bool act = stage_active(st);
+            f32x4 s[KB];
+            if (act) {
+                qk_stage(Kb0, s);
+                xs_put(s, 0);
+            }
+            __syncthreads();   // K reads done, partial scores visible
+            fill_halves(VL, Vh, kbase);
+            if (act) {
+                xs_sum(s, 0);
+                mask_stage(s, kbase);
+                softmax_part(s);
+            }
+            __syncthreads();   // V(st) resident
+            if (act) pv_part(s, Kb0, no_hook);
+            __syncthreads();   // buffer free for the next K
+        }
     } else {
         // Single LDS stage; the next stage's global loads are issued into
         // registers before the current stage computes (D = 1024: its 64
@@ -1898,19 +1984,29 @@ FA_PREFILL_ALL(64)
 FA_PREFILL_ALL(128)
 FA_PREFILL_ALL(256)
 FA_PREFILL_ALL(512)
-// D = 1024: single-stage v3 (no LDS room for a second stage), so no DMA loader
+// D = 1024: one K + V stage fills the LDS; v3's DMA loader alternates the K
+// and V buffers (its scalar / 128-bit loaders run v2's single-stage schedule)
 FA_PREFILL(1024, 1, 0)
 FA_PREFILL(1024, 1, 1)
 FA_PREFILL(1024, 2, 0)
 FA_PREFILL(1024, 2, 1)
 FA_PREFILL(1024, 3, 0)
 FA_PREFILL(1024, 3, 1)
+FA_PREFILL(1024, 3, 2)
 FA_PREFILL_S(1024, 1, 0)
 FA_PREFILL_S(1024, 1, 1)
 FA_PREFILL_S(1024, 2, 0)
 FA_PREFILL_S(1024, 2, 1)
 FA_PREFILL_S(1024, 3, 0)
 FA_PREFILL_S(1024, 3, 1)
+FA_PREFILL_S(1024, 3, 2)
+// D = 2048 (heads of 1025..2048 columns): column groups of 8 waves per
+// 16-row tile; K and V share one LDS buffer; v3 runs v2's schedule
+#define FA_PREFILL_2048(VAR) FA_PREFILL(2048, VAR, 0) FA_PREFILL(2048, VAR, 1) \
+    FA_PREFILL_S(2048, VAR, 0) FA_PREFILL_S(2048, VAR, 1)
+FA_PREFILL_2048(1)
+FA_PREFILL_2048(2)
+FA_PREFILL_2048(3)
 
 // Decode register double-buffering (FA_DECODE_DBUF=1) trades occupancy for
 // one block of loads in flight per register set.
@@ -2012,6 +2108,7 @@ FA_MERGE(128)
 FA_MERGE(256)
 FA_MERGE(512)
 FA_MERGE(1024)
+FA_MERGE(2048)
 
 #define FA_NAIVE(T, SUF)                                                                          \
     extern "C" __global__ void __launch_bounds__(256) fa_naive_scores_##SUF(NaiveParams p) {       \

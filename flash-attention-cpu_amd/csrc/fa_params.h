@@ -83,6 +83,10 @@ constexpr int fa_prefill_stage_keys(int D, int variant) {
 // D = 1024: one 16-key stage of K and V takes 130 KiB of LDS, so v3 keeps a
 // single stage (its math is v2's; only the double-buffered schedule goes).
 constexpr int fa_prefill_nbuf(int D, int variant) { return variant == 3 && D <= 512 ? 2 : 1; }
+// v3 fills its LDS stages by global->LDS DMA (loader 2) up to D = 1024 (two
+// stages up to 512, alternating K / V buffers at 1024); D = 2048 keeps one
+// K-or-V buffer filled through registers for every variant.
+constexpr bool fa_prefill_dma(int D, int variant) { return variant == 3 && D <= 1024; }
 #endif
 
 #endif

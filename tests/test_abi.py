@@ -317,29 +317,35 @@ def test_planning_key_split_prefill():
 
 
 def test_planning_errors():
-    # f32 heads of 257..1024 columns: the column-group flash kernels (forced
+    # f32 heads of 257..2048 columns: the column-group flash kernels (forced
     # prefill and key splits too); split-KV and 16-bit inputs stop at 256
     assert describe(2, 1, 1, 10, 10, 257, False).startswith("fa_prefill_v2_d512_0 grid=1x1x1 block=512")
     assert describe(3, 1, 4, 1000, 1000, 512, True).startswith("fa_prefill_v3_d512_2s ")   # key split
-    assert describe(3, 1, 4, 1000, 1000, 1024, True).startswith("fa_prefill_v3_d1024_1s ")   # one LDS stage
+    assert describe(3, 1, 4, 1000, 1000, 1024, True).startswith("fa_prefill_v3_d1024_2s ")   # K / V buffers alternate
     assert describe(1, 1, 1, 10, 10, 1000, False).startswith("fa_prefill_v1_d1024_1 ")
     assert describe(2, 1, 1, 10, 10, 300, False, fa.PATH_PREFILL).startswith("fa_prefill_v2_d512_1 ")
     s = describe(2, 1, 1, 100, 700, 512, False, fa.PATH_PREFILL, 3)
     assert s.startswith("fa_prefill_v2_d512_1s ") and "fa_merge_d512" in s and "splits=3" in s
     s = describe(3, 1, 1, 100, 700, 1024, False, fa.PATH_PREFILL, 3)
-    assert s.startswith("fa_prefill_v3_d1024_1s ") and "fa_merge_d1024" in s
+    assert s.startswith("fa_prefill_v3_d1024_2s ") and "fa_merge_d1024" in s
     for kw in ({"path": fa.PATH_SPLITKV}, {"path": fa.PATH_SPLITKV_ROWS}, {"dtype": fa.DTYPE_BF16}):
         with pytest.raises(fa.FaError) as e:
             describe(2, 1, 1, 10, 10, 257, False, **kw)
         assert e.value.status == fa.FA_ERR_UNSUPPORTED, kw
     # decode shapes at wide heads stay on the prefill kernels
     assert describe(2, 1, 32, 1, 32768, 512, False).startswith("fa_prefill_v2_d512_1s ")   # key split
-    # wider than 1024: the naive kernels on the automatic path; forced paths
+    # 1025..2048 columns: D = 2048, 16-row workgroups of 8 column-group waves
+    assert describe(2, 1, 1, 10, 10, 1025, False) == "fa_prefill_v2_d2048_0 grid=1x1x1 block=512"
+    assert describe(3, 1, 2, 100, 100, 2048, True) == "fa_prefill_v3_d2048_1 grid=14x1x1 block=512"
+    s = describe(1, 1, 1, 100, 700, 1536, True, fa.PATH_PREFILL, 3)   # v1 key split, all keys per block
+    assert s.startswith("fa_prefill_v1_d2048_1s grid=21x1x1") and "fa_merge_d2048" in s and "splits=3" in s
+    assert describe(2, 1, 1, 40, 300, 1536, True, fa.PATH_STREAM, 7).startswith("fa_prefill_v2_d2048_1s grid=")
+    # wider than 2048: the naive kernels on the automatic path; forced paths
     # and 16-bit inputs are refused
-    assert describe(2, 1, 1, 10, 10, 1025, False).startswith("fa_naive_scores_f32")
+    assert describe(2, 1, 1, 10, 10, 2049, False).startswith("fa_naive_scores_f32")
     for kw in ({"path": fa.PATH_PREFILL}, {"path": fa.PATH_SPLITKV}, {"dtype": fa.DTYPE_BF16}):
         with pytest.raises(fa.FaError) as e:
-            describe(2, 1, 1, 10, 10, 1025, False, **kw)
+            describe(2, 1, 1, 10, 10, 2049, False, **kw)
         assert e.value.status == fa.FA_ERR_UNSUPPORTED, kw
     assert describe(1, 1, 1, 10, 1000, 64, False, fa.PATH_SPLITKV).startswith("fa_decode_v1_d64_2 grid=3x1x1")
     with pytest.raises(fa.FaError) as e:

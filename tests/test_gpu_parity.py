@@ -84,15 +84,15 @@ def test_every_padded_head_dim(variant):
 
 
 def _wide_kernel(d):
-    return 512 if d <= 512 else 1024
+    return 512 if d <= 512 else (1024 if d <= 1024 else 2048)
 
 
 @pytest.mark.parametrize("variant", ALL_VARIANTS)
 def test_wide_heads_run_flash_kernels(variant):
     # The crate's flash path takes any d_head with O(block) scratch
-    # (src/v2.rs:182-189): heads of 257..1024 columns run the column-group
+    # (src/v2.rs:182-189): heads of 257..2048 columns run the column-group
     # flash kernels (no score matrix), odd widths on the scalar loader.
-    for d in (257, 300, 384, 512, 513, 640, 1000, 1023, 1024):
+    for d in (257, 300, 384, 512, 513, 640, 1000, 1023, 1024, 1025, 1536, 2047, 2048):
         plan = fa.describe_launch(variant, 1, 1, 70, 90, d, d % 2 == 1)
         assert plan.startswith(f"fa_prefill_v{variant}_d{_wide_kernel(d)}_"), plan
         run_case(variant, 70, 90, d, 64, 128, d % 2 == 1)
@@ -159,12 +159,35 @@ def test_wide_heads_multiblock_and_key_split(d):
 
 
 @pytest.mark.parametrize("variant", ALL_VARIANTS)
-def test_heads_wider_than_1024_run_naive(variant):
-    # Past the flash kernels' 1024 columns the automatic f32 path runs the
+def test_heads_of_1025_to_2048_columns_run_flash_kernels(variant):
+    """d = 1025, 1536, 2048 (the crate's flash path at any d_head,
+    src/v2.rs:182-189): the D = 2048 kernels -- 16-row workgroups of 8
+    column-group waves, K and V in turn through one LDS buffer -- with no
+    score buffer in the plan; several query blocks, causal and ragged, the key
+    split (automatic on small grids, and forced) and the stream split, every
+    variant against CPU v2 and against each other."""
+    rng = np.random.default_rng(2048 + variant)
+    for bh, sq, sk, d, causal in [(2, 100, 130, 1025, True), (1, 37, 300, 1536, False), (3, 64, 64, 2048, True),
+                                  (1, 200, 90, 2048, False)]:
+        q = rng.standard_normal(bh * sq * d, dtype=np.float32)
+        k = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        v = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+        for path, splits in ((fa.PATH_AUTO, 0), (fa.PATH_PREFILL, 0), (fa.PATH_PREFILL, 3), (fa.PATH_STREAM, 5)):
+            plan = fa.describe_launch(variant, 1, bh, sq, sk, d, causal, path, splits)
+            assert plan.startswith(f"fa_prefill_v{variant}_d2048_") and "naive" not in plan, plan
+            tag = f"v{variant} ({bh},{sq},{sk},{d},{causal}) {plan}"
+            print("[case]", tag, flush=True)
+            assert_parity(_device_run(variant, q, k, v, bh, sq, sk, d, causal, path, splits, guard=64), want, tag)
+
+
+@pytest.mark.parametrize("variant", ALL_VARIANTS)
+def test_heads_wider_than_2048_run_naive(variant):
+    # Past the flash kernels' 2048 columns the automatic f32 path runs the
     # naive kernels (materialised scores, in head chunks capped by free memory).
-    assert fa.describe_launch(variant, 1, 1, 20, 30, 1030, True).startswith("fa_naive_scores_f32")
-    run_case(variant, 20, 30, 1030, 64, 128, True)
-    run_case(variant, 33, 17, 1100, 64, 128, False)
+    assert fa.describe_launch(variant, 1, 1, 20, 30, 2049, True).startswith("fa_naive_scores_f32")
+    run_case(variant, 20, 30, 2049, 64, 128, True)
+    run_case(variant, 33, 17, 2100, 64, 128, False)
 
 
 @pytest.mark.parametrize("variant", ALL_VARIANTS)
@@ -315,7 +338,7 @@ def test_differential_fuzz_split_paths():
 
 
 def test_differential_fuzz_new_paths():
-    """Random shapes through the column-group kernels (d_head 257..1024), the
+    """Random shapes through the column-group kernels (d_head 257..2048), the
     stream split (forced, random workgroup counts) and the LDS-staged split-KV
     tiles (d_head 64 / 128), v2 and v3 against the oracle's CPU v2, with the
     fuzzer's magnitudes for the split paths (fuzz/fuzz_targets/flash_attention.rs:89-126)
@@ -326,7 +349,7 @@ def test_differential_fuzz_new_paths():
         bh = int(rng.integers(1, 4))
         causal = bool(rng.integers(0, 2))
         if kind == 0:      # wide heads
-            d = int(rng.integers(257, 1025))
+            d = int(rng.integers(257, 2049))
             sq, sk = int(rng.integers(1, 300)), int(rng.integers(1, 400))
             path, splits, mag = fa.PATH_AUTO, 0, 1.0
         elif kind == 1:    # stream split
@@ -1002,13 +1025,13 @@ def test_release_stream_workspace_returns_device_memory():
 
 def test_requests_beyond_device_memory_fail_cleanly():
     """FA_ERR_ALLOC before anything is queued, out untouched, the library
-    usable afterwards: (a) the naive path of a d_head > 1024 head whose score
+    usable afterwards: (a) the naive path of a d_head > 2048 head whose score
     matrix (2^19 x 2^19 f32 = 1 TiB) exceeds the device; (b) a forced split
     of 32 heads x 16384 queries x 1024 key splits at d256 (551 GB of
     partials)."""
     torch = _torch()
     dev = torch.device("cuda", 0)
-    n, d = 1 << 19, 1030
+    n, d = 1 << 19, 2050
     q = torch.zeros(n * d, device=dev)
     out = torch.full((n * d,), 5.0, device=dev)
     with pytest.raises(fa.FaError) as e:

@@ -142,9 +142,9 @@ def test_noalloc_refuses_plans_beyond_the_scratch():
         _call(fa.attention_device_noalloc, 2, t, bh, sq, sk, d, False, fa.PATH_SPLITKV, 32)
     assert e.value.status == fa.FA_ERR_SCRATCH
     # d_head beyond the flash kernels (the naive path allocates its score matrix)
-    t = _tensors(1, 8, 8, 1030, 10)
+    t = _tensors(1, 8, 8, 2050, 10)
     with pytest.raises(fa.FaError) as e:
-        _call(fa.attention_device_noalloc, 2, t, 1, 8, 8, 1030, False, fa.PATH_AUTO, 0)
+        _call(fa.attention_device_noalloc, 2, t, 1, 8, 8, 2050, False, fa.PATH_AUTO, 0)
     assert e.value.status == fa.FA_ERR_UNSUPPORTED
 
 
