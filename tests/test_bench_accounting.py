@@ -164,3 +164,30 @@ def test_pmc_table_from_counter_runs(tmp_path):
     path.write_text(json.dumps(table))
     assert traffic.lookup_entry(str(path), "fa_k", 131072)["mfma_busy_pct"] == e["mfma_busy_pct"]
     assert traffic.lookup_entry(str(path), "fa_k", 64) is None
+
+
+def test_profile_report_covers_every_bench_launch(tmp_path):
+    """profile_report plans every benchmark call (f32 variants and 16-bit
+    forms) and lists each (kernel, launch size) of the committed tables
+    under the workloads that launch it; every prefill / decode kernel of the
+    bench has a row in both committed tables (profiles/ measured on the
+    current kernel sources)."""
+    from flash_attention_amd import profile_report as pr
+    calls = pr.workload_launches()
+    labels = {c["label"] for c in calls}
+    for (name, *_rest) in bench.CONFIGS:
+        assert {f"{name} v1", f"{name} v2", f"{name} v3"} <= labels
+    assert {"config2 bf16", "config2 f16", "config3 bf16", "config4a bf16", "config5 f16"} <= labels
+    traffic_t = json.load(open(os.path.join(ROOT, "profiles", "traffic.json")))
+    pmc_t = json.load(open(os.path.join(ROOT, "profiles", "pmc.json")))
+    src = traffic.kernel_source_hash()
+    for c in calls:
+        for k, g in c["launches"]:
+            for t in (traffic_t, pmc_t):
+                e = t.get(f"{k}@{g}")
+                assert e is not None, (c["label"], k, g)
+                assert e["kernel_source_sha256"] == src, (c["label"], k)
+    md = pr.counters_markdown(pmc_t, calls)
+    assert "| fa_prefill_v3_d128_2 | 131072 | config2 v3 |" in md
+    md = pr.traffic_markdown(traffic_t, calls)
+    assert "| fa_prefill_v3_d128_2 | 131072 | config2 v3 |" in md and "134.2 MB" in md
