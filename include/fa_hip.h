@@ -39,8 +39,8 @@ extern "C" {
 #define FA_ERR_OUT_SHAPE 4    /* "out shape mismatch" src/common.rs:54, :90 */
 #define FA_ERR_INVALID_ARG 5  /* NULL pointer with a non-zero length, bad variant/option */
 #define FA_ERR_UNSUPPORTED 6  /* d_head > 256 with 16-bit inputs or a forced split-KV path,
-                                 d_head > 1024 with a forced path / split count, or a size
-                                 beyond 32-bit row indexing (f32 heads up to 1024 run the flash
+                                 d_head > 2048 with a forced path / split count, or a size
+                                 beyond 32-bit row indexing (f32 heads up to 2048 run the flash
                                  kernels; wider ones on the automatic path the naive kernels) */
 #define FA_ERR_NO_DEVICE 7    /* no HIP device visible */
 #define FA_ERR_MODULE 8       /* code object missing / unloadable (FA_HIP_MODULE) */
@@ -122,9 +122,11 @@ int fa_attention_multihead(const float* q, size_t q_len, const float* k, size_t 
  * Same computation as fa_multihead_vN on device pointers (hipMalloc'd or any
  * device-accessible memory), queued on `stream` (a hipStream_t; NULL = the
  * default stream).  No length checks are possible on raw pointers; zero
- * dims return FA_OK with nothing queued.  v2/v3 pick the split-KV
+ * dims return FA_OK with nothing queued.  Every variant picks the split-KV
  * (flash-decoding) kernels for short query blocks against long key ranges,
- * and a key split on grids smaller than the GPU.  Their partials go to a
+ * and a key or stream split on grids smaller than the GPU (v1 on kernels of
+ * its own that keep its per-step normalisation and visit every key, causal
+ * or not).  Their partials go to a
  * workspace kept per stream (up to 256 MiB; larger ones are allocated and
  * released stream-ordered around the call): the first call on a stream that
  * needs more allocates it with hipMalloc, and buffers are kept (outgrown ones
@@ -158,17 +160,18 @@ int fa_release_stream_workspace(void* stream);
 /* ---- extension: explicit scale and path control ------------------------
  * Not in the reference.  softmax_scale <= 0 or NaN keeps the reference's
  * 1/sqrt(d_head).  path: FA_PATH_AUTO (what fa_device_vN does),
- * FA_PATH_PREFILL (query-block kernel; with num_splits > 1 and v2/v3, each
- * block's keys are divided over num_splits workgroups whose partials are
- * merged), FA_PATH_SPLITKV (16-row decode tiles; with one split -- num_splits
- * = 1, or chosen -- each tile is written directly, no merge; v2/v3 only),
- * FA_PATH_SPLITKV_ROWS (row-streaming split-KV for seq_len_q <= 4: K and V
- * read as whole rows, dot products on the vector ALUs; v2/v3, f32, d_head %
- * 4 == 0 and 16-byte aligned operands, else FA_ERR_UNSUPPORTED),
- * FA_PATH_STREAM (query-block kernel with the stream split: the key stages
- * of every (slice, query block) cut into equal runs, one per workgroup --
- * num_splits workgroups, 0 = one per resident workgroup slot -- with
- * partials merged where a block is shared; v2/v3).  AUTO (v2/v3) runs
+ * FA_PATH_PREFILL (query-block kernel; with num_splits > 1, each block's
+ * keys are divided over num_splits workgroups whose partials are merged),
+ * FA_PATH_SPLITKV (16-row decode tiles; with one split -- num_splits = 1, or
+ * chosen -- each tile is written directly, no merge), FA_PATH_SPLITKV_ROWS
+ * (row-streaming split-KV for seq_len_q <= 4: K and V read as whole rows,
+ * dot products on the vector ALUs; f32, d_head % 4 == 0 and 16-byte aligned
+ * operands, else FA_ERR_UNSUPPORTED), FA_PATH_STREAM (query-block kernel
+ * with the stream split: the key stages of every (slice, query block) cut
+ * into equal runs, one per workgroup -- num_splits workgroups, 0 = one per
+ * resident workgroup slot -- with partials merged where a block is shared).
+ * Every path takes every variant; v1's split kernels keep its per-step
+ * normalisation and visit every key (no causal skip).  AUTO runs
  * decode steps -- seq_len_q <= 32, any batch and key count -- on split-KV
  * (the row-streaming kernel where it applies, else 16-row tiles; 16-bit
  * inputs only on the row kernel), and the stream split or the key split for
@@ -201,7 +204,7 @@ int fa_device_ex(int variant, void* stream, const float* q, const float* k, cons
  * but the split partials (split-KV decode, prefill key split) go to a
  * device-global scratch array of 64 MiB per GPU, held until the process
  * ends, and the call allocates and frees nothing.  Calls whose plan needs a
- * larger workspace return FA_ERR_SCRATCH (out untouched); d_head > 1024 (the
+ * larger workspace return FA_ERR_SCRATCH (out untouched); d_head > 2048 (the
  * naive kernels' score matrix) returns FA_ERR_UNSUPPORTED.  Call fa_init()
  * on each device first (it loads the kernels and maps the array; a first
  * call does it itself, which allocates).  All calls on one GPU share its
