@@ -1149,42 +1149,50 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
 // (workgroups + blocks - 1) slots of BQ rows hold them all.  Stage counts per block follow from
 // BQ % SK == 0: block b has R (b + 1) stages (R = BQ / SK) while BQ (b + 1)
 // <= seq_k (causal), otherwise ceil(seq_k / SK).
+// Every unit index fits 32 bits (the host refuses plans whose unit total
+// plus one run passes 2^31), so the quotients below are 32-bit unsigned
+// divisions; products that can pass 2^32 on the way (b (b + 1)) are formed in
+// 64 bits.  Measured (s_memtime in an instrumented copy, 16-bit causal config
+// 2 on the stream split): with 64-bit divisions the decode of a workgroup's
+// first segment took 3.6 us and of each later one 2.2 us.
 struct StreamGeom {
-    long long R, nsf, bf, u_head;
+    unsigned R, nsf, bf, u_head;
     bool causal;
 };
 __device__ __forceinline__ StreamGeom stream_geom(const FaParams& p, int bq, int sk_stage) {
     StreamGeom g;
-    g.R = bq / sk_stage;
-    g.nsf = (p.seq_k + sk_stage - 1) / sk_stage;
-    g.bf = p.seq_k / bq;
+    g.R = (unsigned)(bq / sk_stage);
+    g.nsf = (unsigned)((p.seq_k + sk_stage - 1) / sk_stage);
+    // blocks past the last query block do not exist: a key range longer than
+    // the query range leaves every block on the triangle
+    g.bf = (unsigned)min(p.seq_k / bq, p.nqb);
     g.causal = p.causal != 0 && !p.full_keys;   // v1: every block has all seq_k keys
-    g.u_head = p.stream_head_units;
+    g.u_head = (unsigned)p.stream_head_units;
     return g;
 }
-// units of slice-local blocks 0 .. b-1
-__device__ __forceinline__ long long stream_prefix(const StreamGeom& g, long long b) {
+// units of slice-local blocks 0 .. b-1 (b <= nqb: at most the slice's total)
+__device__ __forceinline__ unsigned stream_prefix(const StreamGeom& g, unsigned b) {
     if (!g.causal) return b * g.nsf;
-    if (b <= g.bf) return g.R * (b * (b + 1) / 2);
-    return g.R * (g.bf * (g.bf + 1) / 2) + (b - g.bf) * g.nsf;
+    if (b <= g.bf) return g.R * (unsigned)(((unsigned long long)b * (b + 1)) >> 1);
+    return g.R * (unsigned)(((unsigned long long)g.bf * (g.bf + 1)) >> 1) + (b - g.bf) * g.nsf;
 }
-__device__ __forceinline__ long long stream_stages(const StreamGeom& g, long long b) {
+__device__ __forceinline__ unsigned stream_stages(const StreamGeom& g, unsigned b) {
     return (g.causal && b < g.bf) ? g.R * (b + 1) : g.nsf;
 }
 // the block holding slice-local unit r
-__device__ __forceinline__ long long stream_block(const StreamGeom& g, long long r) {
+__device__ __forceinline__ unsigned stream_block(const StreamGeom& g, unsigned r) {
     if (!g.causal) return r / g.nsf;
-    const long long tri = g.R * (g.bf * (g.bf + 1) / 2);
+    const unsigned tri = stream_prefix(g, g.bf);
     if (r >= tri) return g.bf + (r - tri) / g.nsf;
-    long long b = (long long)((sqrtf(8.0f * (float)(r / g.R) + 1.0f) - 1.0f) * 0.5f);
+    unsigned b = (unsigned)((sqrtf(8.0f * (float)(r / g.R) + 1.0f) - 1.0f) * 0.5f);
     while (b > 0 && stream_prefix(g, b) > r) --b;
     while (stream_prefix(g, b + 1) <= r) ++b;
     return b;
 }
 // workgroups first .. last share block b of slice h (units [ub, ub + n))
-__device__ __forceinline__ void stream_span(const StreamGeom& g, long long per, long long h, long long b,
-                                            long long& first, long long& last) {
-    const long long ub = h * g.u_head + stream_prefix(g, b);
+__device__ __forceinline__ void stream_span(const StreamGeom& g, unsigned per, unsigned h, unsigned b,
+                                            unsigned& first, unsigned& last) {
+    const unsigned ub = h * g.u_head + stream_prefix(g, b);
     first = ub / per;
     last = (ub + stream_stages(g, b) - 1) / per;
 }
@@ -1201,17 +1209,17 @@ __device__ __forceinline__ void for_each_segment(const FaParams& p, F&& run) {
     // Loop state kept in SGPRs (readfirstlane): it is live across every
     // segment's stage loop, where VGPRs are short.  Unit indices fit 32 bits
     // (the host checks the total).
-    int u = 0, uend = 0, wg = 0;
+    unsigned u = 0, uend = 0, wg = 0;
     if (stream) {
         // Workgroups are dispatched round-robin over the 8 XCDs: consecutive
         // runs (mostly one slice's blocks) go to the same XCD, whose L2 then
         // holds that slice's K / V.
-        const int G = gridDim.x;
-        const int x = blockIdx.x;
+        const unsigned G = gridDim.x;
+        const unsigned x = blockIdx.x;
         wg = (G % 8 == 0) ? (x % 8) * (G / 8) + x / 8 : x;
-        const long long per = p.stream_per;
-        u = (int)(wg * per);
-        uend = (int)min((long long)wg * per + per, (long long)p.bh * p.stream_head_units);
+        const unsigned per = (unsigned)p.stream_per;
+        u = wg * per;
+        uend = min(u + per, (unsigned)p.bh * (unsigned)p.stream_head_units);
     }
     for (int it = 0;; ++it) {
         u = __builtin_amdgcn_readfirstlane(u);
@@ -1221,18 +1229,18 @@ __device__ __forceinline__ void for_each_segment(const FaParams& p, F&& run) {
         if (stream) {
             if (u >= uend) break;
             const StreamGeom sg = stream_geom(p, BQ, SK);
-            const long long h = u / sg.u_head, r = u % sg.u_head;
-            const long long b = stream_block(sg, r);
-            const long long s0 = r - stream_prefix(sg, b);
-            const long long cnt = min(stream_stages(sg, b) - s0, (long long)(uend - u));
-            long long first, last;
-            stream_span(sg, p.stream_per, h, b, first, last);
+            const unsigned h = u / sg.u_head, r = u - h * sg.u_head;
+            const unsigned b = stream_block(sg, r);
+            const unsigned s0 = r - stream_prefix(sg, b);
+            const unsigned cnt = min(stream_stages(sg, b) - s0, uend - u);
+            unsigned first, last;
+            stream_span(sg, (unsigned)p.stream_per, h, b, first, last);
             seg.qb = (int)b;
             seg.bh = (int)h;
             seg.sbeg = (int)s0;
             seg.nst = (int)cnt;
-            seg.slot = first == last ? -1 : (int)(wg + h * p.nqb + b);
-            u += (int)cnt;
+            seg.slot = first == last ? -1 : (int)(wg + h * (unsigned)p.nqb + b);
+            u += cnt;
         } else {
             if (it > 0) break;
             if (STREAM) {   // key split
@@ -1704,8 +1712,8 @@ __device__ __forceinline__ void merge_body(const FaParams& p) {
         // the row), whose partials sit in block slots w + bh * nqb + block
         const StreamGeom sg = stream_geom(p, p.ks_rows, p.split_len);
         const int blk = q / p.ks_rows;
-        long long first, last;
-        stream_span(sg, p.stream_per, bh, blk, first, last);
+        unsigned first, last;
+        stream_span(sg, (unsigned)p.stream_per, (unsigned)bh, (unsigned)blk, first, last);
         if (first == last) return;
         ns = (int)(last - first + 1);
         pstride = (size_t)(p.ks_rows / 16);

@@ -29,8 +29,10 @@ import numpy as np
 import pytest
 
 
-def geom(sk, bq, skk, causal):
-    return {"R": bq // skk, "nsf": -(-sk // skk), "bf": sk // bq, "causal": causal}
+def geom(sk, bq, skk, causal, nqb=None):
+    # the kernel clamps bf to the block count (no block past the last query block exists)
+    bf = sk // bq if nqb is None else min(sk // bq, nqb)
+    return {"R": bq // skk, "nsf": -(-sk // skk), "bf": bf, "causal": causal}
 
 
 def prefix(g, b):
@@ -63,7 +65,7 @@ def block_of(g, r):
 def plan(bh, sq, sk, bq, skk, causal, want):
     """Host side (make_plan's stream_fit)."""
     nqb = -(-sq // bq)
-    g = geom(sk, bq, skk, causal)
+    g = geom(sk, bq, skk, causal, nqb)
     u_head = prefix(g, nqb)
     utot = bh * u_head
     per = max(4, -(-utot // want))
