@@ -63,6 +63,8 @@ CONFIGS = [
     ("wide_d512", 16, 2048, 2048, 512, True, 1.0, False, "prefill"),
     ("wide_d1024", 8, 2048, 2048, 1024, True, 1.0, False, "prefill"),
     ("wide_d2048", 4, 2048, 2048, 2048, True, 1.0, False, "prefill"),
+    # wider than 2048: the any-width kernels (O accumulated in the output)
+    ("wide_d4096", 2, 2048, 2048, 4096, True, 1.0, False, "prefill"),
     # batched decode step: 768 (sequence, head) slices of one query over
     # 2048 keys, the split-KV row kernel whatever the grid size (launch
     # sizes of its own for every variant: profiles key kernels by name and

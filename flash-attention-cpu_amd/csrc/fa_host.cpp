@@ -294,10 +294,13 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     if (lp && variant == 1) return FA_ERR_INVALID_ARG;   // the 16-bit kernels run v2/v3's algorithm
     if (path < FA_PATH_AUTO || path > FA_PATH_STREAM) return FA_ERR_INVALID_ARG;
     if (opts && opts->num_splits < 0) return FA_ERR_INVALID_ARG;
-    if (d > (size_t)kMaxD) return FA_ERR_UNSUPPORTED;
     // d_head > 256: f32 prefill kernels only (column groups; key split allowed)
     const bool wide = d > (size_t)kMaxDNarrow;
     if (wide && (lp || path == FA_PATH_SPLITKV || path == FA_PATH_SPLITKV_ROWS)) return FA_ERR_UNSUPPORTED;
+    // d_head > 2048: the any-width kernels only (one workgroup per 16-row
+    // tile, no split of any kind)
+    const bool any_width = d > (size_t)kMaxD;
+    if (any_width && (path == FA_PATH_STREAM || (opts && opts->num_splits > 1))) return FA_ERR_UNSUPPORTED;
     const size_t imax = 0x7fffffff;
     if (sq > imax || sk > imax || bh > imax) return FA_ERR_UNSUPPORTED;
 
@@ -322,6 +325,22 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
     // src/v1.rs:209-216): its splits count each block's keys as all seq_k.
     p.full_keys = variant == 1 ? 1 : 0;
     const bool causal_skip = causal && variant != 1;
+
+    if (any_width) {
+        // O accumulates in `out` (no workspace); p.nqb counts 16-row tiles
+        const size_t tiles = (sq + 15) / 16;
+        if (tiles * bh > imax || d > imax) return FA_ERR_UNSUPPORTED;
+        const bool vec_any = d % 4 == 0 && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
+        char nm[64];
+        std::snprintf(nm, sizeof(nm), "fa_prefill_v%d_dany_%d", variant, vec_any ? 1 : 0);
+        plan->first.name = nm;
+        plan->first.gx = static_cast<unsigned>(tiles * bh);
+        plan->first.bx = 512;
+        p.nqb = static_cast<int>(tiles);
+        plan->split = false;
+        plan->ws_floats = 0;
+        return FA_OK;
+    }
 
     const size_t rows = (size_t)(lp ? fa_lp_rows() : fa_prefill_rows(D));   // query rows per prefill workgroup
     const size_t nqb = (sq + rows - 1) / rows;
@@ -709,38 +728,14 @@ int stream_workspace(int dev, hipStream_t stream, size_t bytes, void** out) {
     return FA_OK;
 }
 
-int run_naive_device(hipStream_t stream, const float* q, const float* k, const float* v, size_t bh, size_t sq,
-                     size_t sk, size_t d, int causal, int precision, float* out, float scale);
-
-// Heads wider than the flash kernels' 2048 columns (the crate takes any
-// d_head): f32 inputs on the automatic path run the naive kernels over a
-// materialised score matrix (src/naive.rs:14-75, in f32 with the same
-// 1/sqrt(d) or explicit scale), in head chunks capped by free device
-// memory.  FA_OK when that applies, else the status.
-int wide_head_status(int variant, const fa_launch_opts* opts) {
-    if (variant < 1 || variant > 3) return FA_ERR_INVALID_ARG;
-    if (opts && (opts->dtype != FA_DTYPE_F32 || opts->path != FA_PATH_AUTO || opts->num_splits > 0))
-        return FA_ERR_UNSUPPORTED;
-    return FA_OK;
-}
-
 // Queue one attention call on device pointers.  noalloc: the split
 // partials go to the device-global scratch array (fa_scratch.hip) and the
-// call allocates nothing; plans needing more than it holds, and the naive
-// wide-head path, are refused.
+// call allocates nothing; plans needing more than it holds are refused.
 int run_device(int variant, hipStream_t stream, const void* q, const void* k, const void* v, size_t bh,
                size_t sq, size_t sk, size_t d, int causal, const fa_launch_opts* opts, float* out,
                bool noalloc = false) {
     if (bh == 0 || sq == 0 || sk == 0 || d == 0) return FA_OK;   // src/common.rs:56
     if (!q || !k || !v || !out) return FA_ERR_INVALID_ARG;
-    if (d > (size_t)kMaxD && noalloc) return FA_ERR_UNSUPPORTED;
-    if (d > (size_t)kMaxD) {
-        const int rc = wide_head_status(variant, opts);
-        if (rc != FA_OK) return rc;
-        return run_naive_device(stream, static_cast<const float*>(q), static_cast<const float*>(k),
-                                static_cast<const float*>(v), bh, sq, sk, d, causal, FA_NAIVE_F32, out,
-                                opts ? opts->softmax_scale : 0.0f);
-    }
     int dev;
     int rc = current_device(&dev);
     if (rc != FA_OK) return rc;
@@ -1304,14 +1299,8 @@ int fa_describe_launch(int variant, size_t batch, size_t heads, size_t sq, size_
         Plan plan;
         // Alignment is assumed (device allocations are 256-byte aligned).
         static const float dummy[4] __attribute__((aligned(16))) = {0, 0, 0, 0};
-        if (d > (size_t)kMaxD) {
-            rc = wide_head_status(variant, opts);
-            if (rc == FA_OK)
-                text = "fa_naive_scores_f32; fa_naive_softmax_f32; fa_naive_pv_f32 (d_head > 2048: materialised scores)";
-        } else {
-            rc = make_plan(variant, dummy, dummy, dummy, dummy, bh, sq, sk, d, causal, opts, num_cus, &plan);
-        }
-        if (rc == FA_OK && d <= (size_t)kMaxD) {
+        rc = make_plan(variant, dummy, dummy, dummy, dummy, bh, sq, sk, d, causal, opts, num_cus, &plan);
+        if (rc == FA_OK) {
             char tmp[256];
             std::snprintf(tmp, sizeof(tmp), "%s grid=%ux%ux%u block=%u", plan.first.name.c_str(), plan.first.gx,
                           plan.first.gy, plan.first.gz, plan.first.bx);

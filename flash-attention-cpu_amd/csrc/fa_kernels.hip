@@ -1788,6 +1788,195 @@ __device__ __forceinline__ void merge_body(const FaParams& p) {
 #include "fa_decode_rows.inc"
 
 // ---------------------------------------------------------------------------
+// Heads wider than 2048 columns (the crate's flash path takes any d_head,
+// src/v2.rs:175-189, with an O(Br x d) accumulator per query block): one
+// workgroup of NW = 8 waves per 16-row query tile, the unnormalised O
+// accumulator kept in `out` itself (the tile's rows of the caller's [seq_q, d]
+// output), and Q, K and V read from global memory (L2) straight into MFMA
+// operands -- no LDS staging, since each wave reads its own columns.  Per
+// stage of 64 keys:
+//  1. each wave forms partial scores S^T over its 64-column chunks (chunk
+//     ch = wave, wave + NW, ...; a fresh 16-MFMA chain per chunk, added to
+//     the wave's running sum), and the NW partials are summed through LDS
+//     in wave order, so every wave holds bit-identical scores;
+//  2. every wave runs the same online softmax with the exact running max
+//     (src/v2.rs:289-372);
+//  3. each wave reads its chunks of O from `out`, rescales them, adds
+//     V^T P^T and writes them back (lane l owns query row l % 16 and the 16
+//     consecutive columns 16 (l / 16) .. +15 of each chunk).
+// v1 keeps O normalised at every stage (src/v1.rs:313-385) and visits every
+// key; v2 / v3 stop at the tile's causal end and normalise in the last stage
+// (v3's double-buffered LDS stages have nothing to stage here: v3 runs v2's
+// steps).  Columns past d and rows past seq_q / seq_k read as zeros and are
+// never written.
+// ---------------------------------------------------------------------------
+template <int VARIANT, bool VEC>
+__device__ __forceinline__ void prefill_any_body(const FaParams& p) {
+    constexpr int NW = 8;          // waves (column-chunk owners)
+    constexpr int SK = 64;         // keys per stage
+    constexpr int KB = SK / 16;    // 16-key blocks per stage
+    constexpr int CW = 64;         // columns per chunk
+    // partial scores of every wave, two slots (one barrier per stage)
+    __shared__ __attribute__((aligned(16))) f32x4 Xs[2][NW][KB][64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, li = lane & 15;
+    int qt, bh;
+    map_block(p, blockIdx.x, qt, bh);   // p.nqb: 16-row tiles per slice
+    const int seq_q = p.seq_q, seq_k = p.seq_k, d = p.d;
+    const float* __restrict__ Qh = p.q + (size_t)bh * seq_q * d;
+    const float* __restrict__ Kh = p.k + (size_t)bh * seq_k * d;
+    const float* __restrict__ Vh = p.v + (size_t)bh * seq_k * d;
+    float* __restrict__ Oh = p.out + (size_t)bh * seq_q * d;
+    const int row0 = qt * 16, qrow = row0 + li;
+    const bool row_ok = qrow < seq_q;
+    const bool causal = p.causal != 0;
+    const float c = p.scale_log2e;
+    // v1 visits every key (src/v1.rs:209-216); v2 / v3 stop after the
+    // tile's last row (src/v2.rs:208-212)
+    const int kend = (VARIANT != 1 && causal) ? min(seq_k, row0 + 16) : seq_k;
+    const int nst = (kend + SK - 1) / SK;
+    const int nch = (d + CW - 1) / CW;
+    float* const orow = Oh + (size_t)qrow * d;
+
+    // O chunk of this lane: o[j][r] = O[qrow][col0 + 16 g + 4 r + j]
+    auto load_o = [&](int col0, f32x4* o) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const f32x4 t = load4<VEC>(Oh, qrow, seq_q, col0 + 16 * g + 4 * r, d);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j][r] = t[j];
+        }
+    };
+    auto store_o = [&](int col0, const f32x4* o) {
+        if (!row_ok) return;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int col = col0 + 16 * g + 4 * r;
+            if (VEC && col < d) {
+                *reinterpret_cast<f32x4*>(orow + col) = (f32x4){o[0][r], o[1][r], o[2][r], o[3][r]};
+            } else if (!VEC) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (col + j < d) orow[col + j] = o[j][r];
+            }
+        }
+    };
+
+    float m = FA_NEG_INF;   // running max of the row's log2-domain scores
+    float l = 0.0f;         // running row sum (v1: of the normalised accumulator)
+    for (int st = 0; st < nst; ++st) {
+        const int kbase = st * SK;
+        const int slot = st & 1;
+        // 1. this wave's partial scores
+        f32x4 s[KB];
+#pragma unroll
+        for (int b = 0; b < KB; ++b) s[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int ch = wave; ch < nch; ch += NW) {
+            f32x4 t[KB];
+#pragma unroll
+            for (int b = 0; b < KB; ++b) t[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int cc = 0; cc < CW / 16; ++cc) {
+                const int col = ch * CW + 16 * cc + 4 * g;
+                const f32x4 qv = load4<VEC>(Qh, qrow, seq_q, col, d);
+                f32x4 kv[KB];
+#pragma unroll
+                for (int b = 0; b < KB; ++b) kv[b] = load4<VEC>(Kh, kbase + 16 * b + li, seq_k, col, d);
+#pragma unroll
+                for (int b = 0; b < KB; ++b)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) t[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[b][i], qv[i], t[b], 0, 0, 0);
+            }
+#pragma unroll
+            for (int b = 0; b < KB; ++b) s[b] += t[b];
+        }
+#pragma unroll
+        for (int b = 0; b < KB; ++b) Xs[slot][wave][b][lane] = s[b];
+        __syncthreads();
+#pragma unroll
+        for (int b = 0; b < KB; ++b) {
+            f32x4 x = Xs[slot][0][b][lane];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) x += Xs[slot][w][b][lane];
+            s[b] = x;
+        }
+        // 2. online softmax: scores in the log2 domain (dot * scale * log2 e),
+        // keys past seq_k and, causal, past the row masked (top-left aligned,
+        // src/naive.rs:37)
+        float mt = FA_NEG_INF;
+#pragma unroll
+        for (int b = 0; b < KB; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = kbase + 16 * b + 4 * g + r;
+                const float x = (key >= seq_k || (causal && key > qrow)) ? FA_NEG_INF : s[b][r] * c;
+                s[b][r] = x;
+                mt = fmaxf(mt, x);
+            }
+        mt = row4_max(mt);
+        const float m_new = fmaxf(m, mt);
+        const float corr = rescale_factor(m, m_new, 1.0f);   // 0 while the row has seen no key
+        const float mref = (m_new == FA_NEG_INF) ? 0.0f : m_new;
+        float ps = 0.0f;
+#pragma unroll
+        for (int b = 0; b < KB; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                s[b][r] = fa_exp2(s[b][r] - mref);
+                ps += s[b][r];
+            }
+        const float rs = row4_sum(ps);
+        const float l_new = l * corr + rs;
+        const bool last = st + 1 == nst;
+        // factors on the stored O before and after this stage's PV
+        float f_pre, f_post;
+        bool moves = true;
+        if (VARIANT == 1) {
+            // un-normalise by l * corr, add PV, re-normalise by 1 / l_new;
+            // a stage that adds nothing to the row and does not move its max
+            // is an identity and is skipped (no rounding drift)
+            moves = m_new != m || rs != 0.0f;
+            f_pre = l * corr;
+            f_post = l_new > 0.0f ? 1.0f / l_new : 0.0f;
+        } else {
+            f_pre = corr;
+            f_post = last ? (l_new > 0.0f ? 1.0f / l_new : 0.0f) : 1.0f;
+        }
+        m = m_new;
+        l = l_new;
+        // 3. this wave's chunks of O (the whole wave skips when no row moves)
+        if (__builtin_amdgcn_ballot_w64(moves) != 0) {
+            for (int ch = wave; ch < nch; ch += NW) {
+                const int col0 = ch * CW;
+                f32x4 o[4];
+                if (st == 0 || !row_ok) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) o[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+                } else {
+                    load_o(col0, o);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) o[j] *= f_pre;
+                }
+#pragma unroll
+                for (int step = 0; step < 4 * KB; ++step) {
+                    const int key = kbase + 16 * (step / 4) + 4 * g + (step % 4);
+                    const f32x4 vv = load4<VEC>(Vh, key, seq_k, col0 + 4 * li, d);
+                    const float pr = s[step / 4][step % 4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[j], pr, o[j], 0, 0, 0);
+                }
+                if (VARIANT == 1 || last) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) o[j] *= f_post;
+                }
+                if (moves) store_o(col0, o);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Naive attention: the textbook three passes over a materialised score
 // matrix (src/naive.rs:14-75), kept as an on-device reference -- in f32 as
 // the crate computes it, or in f64 to check the fast kernels on shapes too
@@ -2015,6 +2204,18 @@ FA_PREFILL_S(1024, 3, 2)
 FA_PREFILL_2048(1)
 FA_PREFILL_2048(2)
 FA_PREFILL_2048(3)
+// Heads wider than 2048 columns: fa_prefill_v{V}_dany_{L}, L = 0 scalar
+// loads (any d), 1 vector loads (d % 4 == 0, 16-byte aligned operands)
+#define FA_PREFILL_ANY(VAR, LD)                                                                  \
+    extern "C" __global__ void __launch_bounds__(512, 2) fa_prefill_v##VAR##_dany_##LD(FaParams p) {  \
+        prefill_any_body<VAR, LD != 0>(p);                                                       \
+    }
+FA_PREFILL_ANY(1, 0)
+FA_PREFILL_ANY(1, 1)
+FA_PREFILL_ANY(2, 0)
+FA_PREFILL_ANY(2, 1)
+FA_PREFILL_ANY(3, 0)
+FA_PREFILL_ANY(3, 1)
 
 // Decode register double-buffering (FA_DECODE_DBUF=1) trades occupancy for
 // one block of loads in flight per register set.

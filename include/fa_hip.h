@@ -39,9 +39,9 @@ extern "C" {
 #define FA_ERR_OUT_SHAPE 4    /* "out shape mismatch" src/common.rs:54, :90 */
 #define FA_ERR_INVALID_ARG 5  /* NULL pointer with a non-zero length, bad variant/option */
 #define FA_ERR_UNSUPPORTED 6  /* d_head > 256 with 16-bit inputs or a forced split-KV path,
-                                 d_head > 2048 with a forced path / split count, or a size
-                                 beyond 32-bit row indexing (f32 heads up to 2048 run the flash
-                                 kernels; wider ones on the automatic path the naive kernels) */
+                                 d_head > 2048 with a forced stream split or a split count, or a
+                                 size beyond 32-bit row indexing (f32 heads of any width run the
+                                 flash kernels) */
 #define FA_ERR_NO_DEVICE 7    /* no HIP device visible */
 #define FA_ERR_MODULE 8       /* code object missing / unloadable (FA_HIP_MODULE) */
 #define FA_ERR_ALLOC 9        /* device allocation failed, or the request exceeds the free
@@ -204,8 +204,7 @@ int fa_device_ex(int variant, void* stream, const float* q, const float* k, cons
  * but the split partials (split-KV decode, prefill key split) go to a
  * device-global scratch array of 64 MiB per GPU, held until the process
  * ends, and the call allocates and frees nothing.  Calls whose plan needs a
- * larger workspace return FA_ERR_SCRATCH (out untouched); d_head > 2048 (the
- * naive kernels' score matrix) returns FA_ERR_UNSUPPORTED.  Call fa_init()
+ * larger workspace return FA_ERR_SCRATCH (out untouched).  Call fa_init()
  * on each device first (it loads the kernels and maps the array; a first
  * call does it itself, which allocates).  All calls on one GPU share its
  * array: calls that may overlap on one GPU (different streams, or graphs

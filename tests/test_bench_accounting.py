@@ -33,6 +33,7 @@ STATED = {   # name: (GFLOP, bytes)
     "wide_d512": (68.753, 268435456),
     "wide_d1024": (68.753, 268435456),
     "wide_d2048": (68.753, 268435456),
+    "wide_d4096": (68.753, 268435456),
     # 4 * 128 * 2048 * 768; 4 * 768 * 128 * (2 * 1 + 2 * 2048)
     "decode_batched": (0.80531, 1611399168),
 }

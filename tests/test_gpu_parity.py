@@ -182,12 +182,36 @@ def test_heads_of_1025_to_2048_columns_run_flash_kernels(variant):
 
 
 @pytest.mark.parametrize("variant", ALL_VARIANTS)
-def test_heads_wider_than_2048_run_naive(variant):
-    # Past the flash kernels' 2048 columns the automatic f32 path runs the
-    # naive kernels (materialised scores, in head chunks capped by free memory).
-    assert fa.describe_launch(variant, 1, 1, 20, 30, 2049, True).startswith("fa_naive_scores_f32")
+def test_heads_wider_than_2048_run_flash_kernels(variant):
+    """d > 2048 (the crate's flash path at any d_head, src/v2.rs:175-189):
+    the any-width kernels -- one workgroup per 16-row tile, O accumulated in
+    the output rows -- with no score buffer and no workspace.  Widths with a
+    ragged last 64-column chunk and with d % 4 != 0 (scalar loads), ragged
+    query tiles, key ends inside a 64-key stage, causal with seq_q < seq_k
+    and > seq_k, several slices; every variant against CPU v2 and the f64
+    naive oracle; forced prefill path as the automatic one."""
+    rng = np.random.default_rng(4096 + variant)
+    for bh, sq, sk, d, causal in [(1, 20, 30, 2049, True), (1, 33, 17, 2100, False), (2, 40, 100, 3000, True),
+                                  (1, 70, 45, 4096, True), (2, 17, 130, 2052, False)]:
+        q = rng.standard_normal(bh * sq * d, dtype=np.float32)
+        k = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        v = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+        for path in (fa.PATH_AUTO, fa.PATH_PREFILL):
+            plan = fa.describe_launch(variant, 1, bh, sq, sk, d, causal, path)
+            assert plan.startswith(f"fa_prefill_v{variant}_dany_{1 if d % 4 == 0 else 0} ") and \
+                "workspace" not in plan, plan
+            tag = f"v{variant} ({bh},{sq},{sk},{d},{causal}) {plan}"
+            print("[case]", tag, flush=True)
+            got = _device_run(variant, q, k, v, bh, sq, sk, d, causal, path, 0, guard=64)
+            assert_parity(got, want, tag)
+        for h in range(bh):
+            sl_q = slice(h * sq * d, (h + 1) * sq * d)
+            sl_k = slice(h * sk * d, (h + 1) * sk * d)
+            naive = oracle.naive_f64(q[sl_q], k[sl_k], v[sl_k], sq, sk, d, causal)
+            assert max_abs_diff(got[sl_q], naive) < NAIVE_TOL, tag
+    # the host-slice entry point takes the same kernels
     run_case(variant, 20, 30, 2049, 64, 128, True)
-    run_case(variant, 33, 17, 2100, 64, 128, False)
 
 
 @pytest.mark.parametrize("variant", ALL_VARIANTS)
@@ -1025,7 +1049,7 @@ def test_release_stream_workspace_returns_device_memory():
 
 def test_requests_beyond_device_memory_fail_cleanly():
     """FA_ERR_ALLOC before anything is queued, out untouched, the library
-    usable afterwards: (a) the naive path of a d_head > 2048 head whose score
+    usable afterwards: (a) naive attention on device pointers whose score
     matrix (2^19 x 2^19 f32 = 1 TiB) exceeds the device; (b) a forced split
     of 32 heads x 16384 queries x 1024 key splits at d256 (551 GB of
     partials)."""
@@ -1035,8 +1059,8 @@ def test_requests_beyond_device_memory_fail_cleanly():
     q = torch.zeros(n * d, device=dev)
     out = torch.full((n * d,), 5.0, device=dev)
     with pytest.raises(fa.FaError) as e:
-        fa.attention_device(2, q.data_ptr(), q.data_ptr(), q.data_ptr(), 1, 1, n, n, d, False, out.data_ptr(),
-                            torch.cuda.current_stream().cuda_stream)
+        fa.naive_device(q.data_ptr(), q.data_ptr(), q.data_ptr(), 1, 1, n, n, d, False, out.data_ptr(),
+                        torch.cuda.current_stream().cuda_stream)
     assert e.value.status == fa.FA_ERR_ALLOC
     torch.cuda.synchronize()
     assert bool((out == 5.0).all())

@@ -141,11 +141,18 @@ def test_noalloc_refuses_plans_beyond_the_scratch():
     with pytest.raises(fa.FaError) as e:
         _call(fa.attention_device_noalloc, 2, t, bh, sq, sk, d, False, fa.PATH_SPLITKV, 32)
     assert e.value.status == fa.FA_ERR_SCRATCH
-    # d_head beyond the flash kernels (the naive path allocates its score matrix)
-    t = _tensors(1, 8, 8, 2050, 10)
-    with pytest.raises(fa.FaError) as e:
-        _call(fa.attention_device_noalloc, 2, t, 1, 8, 8, 2050, False, fa.PATH_AUTO, 0)
-    assert e.value.status == fa.FA_ERR_UNSUPPORTED
+
+
+def test_noalloc_heads_wider_than_2048_need_no_scratch():
+    """Heads wider than 2048 columns accumulate O in the output rows: the
+    no-alloc entry point runs them as fa_device_ex does, bit for bit."""
+    fa.init()
+    bh, sq, sk, d = 2, 40, 70, 2050
+    assert "workspace=" not in fa.describe_launch(2, 1, bh, sq, sk, d, True)
+    t = _tensors(bh, sq, sk, d, 10)
+    want = _call(fa.attention_device, 2, t, bh, sq, sk, d, True, fa.PATH_AUTO, 0)
+    got = _call(fa.attention_device_noalloc, 2, t, bh, sq, sk, d, True, fa.PATH_AUTO, 0)
+    assert np.array_equal(got, want)
 
 
 def test_noalloc_prefill_without_split_needs_no_scratch():
