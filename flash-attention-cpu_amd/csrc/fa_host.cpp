@@ -332,7 +332,9 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
         if (tiles * bh > imax || d > imax) return FA_ERR_UNSUPPORTED;
         const bool vec_any = d % 4 == 0 && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
         char nm[64];
-        std::snprintf(nm, sizeof(nm), "fa_prefill_v%d_dany_%d", variant, vec_any ? 1 : 0);
+        // up to 4096 columns (8 waves x 8 chunks of 64) each wave keeps its
+        // chunks of O in registers; wider heads accumulate in `out`
+        std::snprintf(nm, sizeof(nm), "fa_prefill_v%d_%s_%d", variant, d <= 4096 ? "dreg" : "dany", vec_any ? 1 : 0);
         plan->first.name = nm;
         plan->first.gx = static_cast<unsigned>(tiles * bh);
         plan->first.bx = 512;

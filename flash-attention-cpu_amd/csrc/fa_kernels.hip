@@ -1810,7 +1810,10 @@ __device__ __forceinline__ void merge_body(const FaParams& p) {
 // steps).  Columns past d and rows past seq_q / seq_k read as zeros and are
 // never written.
 // ---------------------------------------------------------------------------
-template <int VARIANT, bool VEC>
+// NCR > 0 (heads of at most NW * NCR * 64 columns): each wave keeps its NCR
+// chunks of O in registers for the whole kernel instead -- no read-modify-
+// write of `out` per stage -- and writes them once at the end.
+template <int VARIANT, bool VEC, int NCR>
 __device__ __forceinline__ void prefill_any_body(const FaParams& p) {
     constexpr int NW = 8;          // waves (column-chunk owners)
     constexpr int SK = 64;         // keys per stage
@@ -1865,6 +1868,22 @@ __device__ __forceinline__ void prefill_any_body(const FaParams& p) {
 
     float m = FA_NEG_INF;   // running max of the row's log2-domain scores
     float l = 0.0f;         // running row sum (v1: of the normalised accumulator)
+    f32x4 oreg[NCR > 0 ? NCR : 1][4];   // register-held chunks: ch = wave + NW j
+#pragma unroll
+    for (int j = 0; j < (NCR > 0 ? NCR : 1); ++j)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) oreg[j][jj] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    // O^T += V^T P^T for one chunk (64 columns from col0) over the stage's keys
+    auto pv_chunk = [&](const f32x4* s_, int kbase, int col0, f32x4* o) {
+#pragma unroll
+        for (int step = 0; step < 4 * KB; ++step) {
+            const int key = kbase + 16 * (step / 4) + 4 * g + (step % 4);
+            const f32x4 vv = load4<VEC>(Vh, key, seq_k, col0 + 4 * li, d);
+            const float pr = s_[step / 4][step % 4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[j], pr, o[j], 0, 0, 0);
+        }
+    };
     for (int st = 0; st < nst; ++st) {
         const int kbase = st * SK;
         const int slot = st & 1;
@@ -1928,7 +1947,7 @@ __device__ __forceinline__ void prefill_any_body(const FaParams& p) {
             }
         const float rs = row4_sum(ps);
         const float l_new = l * corr + rs;
-        const bool last = st + 1 == nst;
+        const bool last = NCR == 0 && st + 1 == nst;   // register-held O is normalised at the end
         // factors on the stored O before and after this stage's PV
         float f_pre, f_post;
         bool moves = true;
@@ -1947,30 +1966,54 @@ __device__ __forceinline__ void prefill_any_body(const FaParams& p) {
         l = l_new;
         // 3. this wave's chunks of O (the whole wave skips when no row moves)
         if (__builtin_amdgcn_ballot_w64(moves) != 0) {
-            for (int ch = wave; ch < nch; ch += NW) {
-                const int col0 = ch * CW;
+            if constexpr (NCR > 0) {
+                // rows that do not move keep their accumulator as it is
+                const float fa = moves ? f_pre : 1.0f;
+                const float fb = moves ? f_post : 1.0f;
+#pragma unroll
+                for (int j = 0; j < NCR; ++j) {
+                    if (wave + NW * j < nch) {
+#pragma unroll
+                        for (int jj = 0; jj < 4; ++jj) oreg[j][jj] *= fa;
+                        pv_chunk(s, kbase, (wave + NW * j) * CW, oreg[j]);
+                        if (VARIANT == 1) {
+#pragma unroll
+                            for (int jj = 0; jj < 4; ++jj) oreg[j][jj] *= fb;
+                        }
+                    }
+                }
+            } else {
+                for (int ch = wave; ch < nch; ch += NW) {
+                    const int col0 = ch * CW;
+                    f32x4 o[4];
+                    if (st == 0 || !row_ok) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) o[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+                    } else {
+                        load_o(col0, o);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) o[j] *= f_pre;
+                    }
+                    pv_chunk(s, kbase, col0, o);
+                    if (VARIANT == 1 || last) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) o[j] *= f_post;
+                    }
+                    if (moves) store_o(col0, o);
+                }
+            }
+        }
+    }
+    if constexpr (NCR > 0) {
+        // v2 / v3: the final normalisation; v1's accumulator is normalised
+        const float inv = VARIANT == 1 ? 1.0f : (l > 0.0f ? 1.0f / l : 0.0f);
+#pragma unroll
+        for (int j = 0; j < NCR; ++j) {
+            if (wave + NW * j < nch) {
                 f32x4 o[4];
-                if (st == 0 || !row_ok) {
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) o[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-                } else {
-                    load_o(col0, o);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) o[j] *= f_pre;
-                }
-#pragma unroll
-                for (int step = 0; step < 4 * KB; ++step) {
-                    const int key = kbase + 16 * (step / 4) + 4 * g + (step % 4);
-                    const f32x4 vv = load4<VEC>(Vh, key, seq_k, col0 + 4 * li, d);
-                    const float pr = s[step / 4][step % 4];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[j], pr, o[j], 0, 0, 0);
-                }
-                if (VARIANT == 1 || last) {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) o[j] *= f_post;
-                }
-                if (moves) store_o(col0, o);
+                for (int jj = 0; jj < 4; ++jj) o[jj] = oreg[j][jj] * inv;
+                store_o((wave + NW * j) * CW, o);
             }
         }
     }
@@ -2204,11 +2247,16 @@ FA_PREFILL_S(1024, 3, 2)
 FA_PREFILL_2048(1)
 FA_PREFILL_2048(2)
 FA_PREFILL_2048(3)
-// Heads wider than 2048 columns: fa_prefill_v{V}_dany_{L}, L = 0 scalar
-// loads (any d), 1 vector loads (d % 4 == 0, 16-byte aligned operands)
+// Heads wider than 2048 columns: fa_prefill_v{V}_dany_{L} (any d, O in the
+// output rows) and fa_prefill_v{V}_dreg_{L} (d <= 4096, O in registers);
+// L = 0 scalar loads (any d), 1 vector loads (d % 4 == 0, 16-byte aligned
+// operands)
 #define FA_PREFILL_ANY(VAR, LD)                                                                  \
     extern "C" __global__ void __launch_bounds__(512, 2) fa_prefill_v##VAR##_dany_##LD(FaParams p) {  \
-        prefill_any_body<VAR, LD != 0>(p);                                                       \
+        prefill_any_body<VAR, LD != 0, 0>(p);                                                    \
+    }                                                                                            \
+    extern "C" __global__ void __launch_bounds__(512, 1) fa_prefill_v##VAR##_dreg_##LD(FaParams p) {  \
+        prefill_any_body<VAR, LD != 0, 8>(p);                                                    \
     }
 FA_PREFILL_ANY(1, 0)
 FA_PREFILL_ANY(1, 1)

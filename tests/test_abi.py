@@ -341,10 +341,13 @@ def test_planning_errors():
     assert s.startswith("fa_prefill_v1_d2048_1s grid=21x1x1") and "fa_merge_d2048" in s and "splits=3" in s
     assert describe(2, 1, 1, 40, 300, 1536, True, fa.PATH_STREAM, 7).startswith("fa_prefill_v2_d2048_1s grid=")
     # wider than 2048: the any-width flash kernels, one 8-wave workgroup per
-    # 16-row query tile and slice (no workspace); scalar loads unless d % 4 == 0
-    assert describe(2, 1, 1, 10, 10, 2049, False) == "fa_prefill_v2_dany_0 grid=1x1x1 block=512"
-    assert describe(1, 2, 3, 100, 700, 4096, True) == "fa_prefill_v1_dany_1 grid=42x1x1 block=512"
-    assert describe(3, 1, 1, 33, 9, 2052, True, fa.PATH_PREFILL).startswith("fa_prefill_v3_dany_1 grid=3x1x1")
+    # 16-row query tile and slice (no workspace); O in registers up to 4096
+    # columns, in the output rows beyond; scalar loads unless d % 4 == 0
+    assert describe(2, 1, 1, 10, 10, 2049, False) == "fa_prefill_v2_dreg_0 grid=1x1x1 block=512"
+    assert describe(1, 2, 3, 100, 700, 4096, True) == "fa_prefill_v1_dreg_1 grid=42x1x1 block=512"
+    assert describe(3, 1, 1, 33, 9, 2052, True, fa.PATH_PREFILL).startswith("fa_prefill_v3_dreg_1 grid=3x1x1")
+    assert describe(2, 1, 1, 10, 10, 4097, False) == "fa_prefill_v2_dany_0 grid=1x1x1 block=512"
+    assert describe(3, 1, 2, 40, 40, 10000, True).startswith("fa_prefill_v3_dany_1 grid=6x1x1")
     # forced splits and 16-bit inputs are refused
     for kw in ({"path": fa.PATH_STREAM}, {"path": fa.PATH_SPLITKV}, {"path": fa.PATH_SPLITKV_ROWS},
                {"path": fa.PATH_PREFILL, "splits": 3}, {"dtype": fa.DTYPE_BF16}):

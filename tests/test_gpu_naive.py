@@ -166,12 +166,14 @@ def test_config5_every_row_against_naive_f64():
 
 
 def test_heads_wider_than_2048_every_row_against_naive_f64():
-    """The any-width flash kernels (O accumulated in the output rows) at the
-    bench row's width, d = 4096, and a width with a ragged last 64-column
-    chunk and d % 4 != 0 (d = 3001: scalar loads), causal and not, every row
-    of every variant against the f64 naive on the GPU; keys end inside a
-    64-key stage."""
-    for bh, sq, sk, d, causal in [(2, 300, 300, 4096, True), (1, 257, 130, 3001, False), (2, 200, 211, 3001, True)]:
+    """The any-width flash kernels at the bench row's width, d = 4096, at a
+    width with a ragged last 64-column chunk and d % 4 != 0 (d = 3001: scalar
+    loads) -- O in registers -- and past 4096 (O accumulated in the output
+    rows), causal and not, every row of every variant against the f64 naive
+    on the GPU; keys end inside a 64-key stage."""
+    for bh, sq, sk, d, causal in [(2, 300, 300, 4096, True), (1, 257, 130, 3001, False), (2, 200, 211, 3001, True),
+                                  (1, 150, 160, 4500, True)]:
         q, k, v = normal_vec(bh * sq * d, 11), normal_vec(bh * sk * d, 12), normal_vec(bh * sk * d, 13)
-        assert fa.describe_launch(3, 1, bh, sq, sk, d, causal).startswith("fa_prefill_v3_dany_")
+        plan = fa.describe_launch(3, 1, bh, sq, sk, d, causal)
+        assert plan.startswith("fa_prefill_v3_dreg_" if d <= 4096 else "fa_prefill_v3_dany_"), plan
         _flash_vs_naive_f64(bh, sq, sk, d, causal, q, k, v)

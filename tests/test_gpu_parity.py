@@ -185,21 +185,24 @@ def test_heads_of_1025_to_2048_columns_run_flash_kernels(variant):
 def test_heads_wider_than_2048_run_flash_kernels(variant):
     """d > 2048 (the crate's flash path at any d_head, src/v2.rs:175-189):
     the any-width kernels -- one workgroup per 16-row tile, O accumulated in
-    the output rows -- with no score buffer and no workspace.  Widths with a
-    ragged last 64-column chunk and with d % 4 != 0 (scalar loads), ragged
-    query tiles, key ends inside a 64-key stage, causal with seq_q < seq_k
-    and > seq_k, several slices; every variant against CPU v2 and the f64
-    naive oracle; forced prefill path as the automatic one."""
+    registers up to 4096 columns, in the output rows beyond -- with no score
+    buffer and no workspace.  Widths with a ragged last 64-column chunk and
+    with d % 4 != 0 (scalar loads), ragged query tiles, key ends inside a
+    64-key stage, causal with seq_q < seq_k and > seq_k, several slices,
+    waves with fewer chunks than others; every variant against CPU v2 and the
+    f64 naive oracle; forced prefill path as the automatic one."""
     rng = np.random.default_rng(4096 + variant)
     for bh, sq, sk, d, causal in [(1, 20, 30, 2049, True), (1, 33, 17, 2100, False), (2, 40, 100, 3000, True),
-                                  (1, 70, 45, 4096, True), (2, 17, 130, 2052, False)]:
+                                  (1, 70, 45, 4096, True), (2, 17, 130, 2052, False), (1, 30, 70, 4097, True),
+                                  (1, 19, 50, 5000, False)]:
         q = rng.standard_normal(bh * sq * d, dtype=np.float32)
         k = rng.standard_normal(bh * sk * d, dtype=np.float32)
         v = rng.standard_normal(bh * sk * d, dtype=np.float32)
         want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
         for path in (fa.PATH_AUTO, fa.PATH_PREFILL):
             plan = fa.describe_launch(variant, 1, bh, sq, sk, d, causal, path)
-            assert plan.startswith(f"fa_prefill_v{variant}_dany_{1 if d % 4 == 0 else 0} ") and \
+            kind = "dreg" if d <= 4096 else "dany"
+            assert plan.startswith(f"fa_prefill_v{variant}_{kind}_{1 if d % 4 == 0 else 0} ") and \
                 "workspace" not in plan, plan
             tag = f"v{variant} ({bh},{sq},{sk},{d},{causal}) {plan}"
             print("[case]", tag, flush=True)
