@@ -1101,7 +1101,7 @@ const char* fa_status_string(int status) {
         case FA_ERR_V_SHAPE: return "v shape mismatch";
         case FA_ERR_OUT_SHAPE: return "out shape mismatch";
         case FA_ERR_INVALID_ARG: return "invalid argument";
-        case FA_ERR_UNSUPPORTED: return "unsupported shape (d_head > 256 with 16-bit inputs or split-KV, d_head > 2048 off the automatic f32 path, or size beyond 32-bit indexing)";
+        case FA_ERR_UNSUPPORTED: return "unsupported shape (d_head > 256 with 16-bit inputs or split-KV, d_head > 2048 with a stream split or split count, or size beyond 32-bit indexing)";
         case FA_ERR_NO_DEVICE: return "no HIP device available";
         case FA_ERR_MODULE: return "cannot load the gfx950 code object (fa_kernels.hsaco / FA_HIP_MODULE)";
         case FA_ERR_ALLOC: return "device allocation failed";
