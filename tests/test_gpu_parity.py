@@ -217,6 +217,35 @@ def test_heads_wider_than_2048_run_flash_kernels(variant):
     run_case(variant, 20, 30, 2049, 64, 128, True)
 
 
+def test_heads_wider_than_2048_differential_fuzz():
+    """Random shapes on the any-width kernels: d_head 2049..6000 (O in
+    registers up to 4096 columns, in the output rows beyond; scalar loads
+    when d % 4 != 0), 1..4 slices, ragged query and key counts (a query tile
+    or 64-key stage cut anywhere), causal or not, logits up to sigma 2;
+    v1 / v2 / v3 against CPU v2, and v2 / v3 bit-identical (v3 runs v2's
+    steps on these kernels)."""
+    rng = np.random.default_rng(6000)
+    for case in range(8):
+        d = int(rng.integers(2049, 6001))
+        bh = int(rng.integers(1, 5))
+        sq, sk = int(rng.integers(1, 150)), int(rng.integers(1, 200))
+        causal = bool(rng.integers(0, 2))
+        sigma = float(rng.choice([0.5, 1.0, 2.0]))
+        q = (rng.standard_normal(bh * sq * d) * sigma).astype(np.float32)
+        k = (rng.standard_normal(bh * sk * d) * sigma).astype(np.float32)
+        v = rng.uniform(-1, 1, bh * sk * d).astype(np.float32)
+        want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+        got = {}
+        for variant in ALL_VARIANTS:
+            plan = fa.describe_launch(variant, 1, bh, sq, sk, d, causal)
+            tag = f"fuzz {case}: v{variant} ({bh},{sq},{sk},{d},{causal}) sigma={sigma} {plan}"
+            print("[case]", tag, flush=True)
+            assert ("_dreg_" if d <= 4096 else "_dany_") in plan, plan
+            got[variant] = _device_run(variant, q, k, v, bh, sq, sk, d, causal, guard=64)
+            assert_parity(got[variant], want, tag)
+        assert np.array_equal(got[2], got[3]), case
+
+
 @pytest.mark.parametrize("variant", ALL_VARIANTS)
 def test_multihead_matches_per_head(variant):
     batch, heads, seq_q, seq_k, d = 2, 3, 37, 50, 16
