@@ -395,8 +395,17 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
 #pragma unroll
         for (int i = 0; i < NQ; ++i) qreg[i] *= c;
     };
-    load_q(qrow);
-    scale_q();
+    // LATE_Q (v3 with the DMA loader, D = 128 and 256, split kernels too): Q
+    // is loaded after the first stages' DMA is issued and scaled chunk by
+    // chunk inside stage 0's QK^T, so the first MFMAs wait for K(0) and Q's
+    // first chunk only (below).  Measured on MI355X, bit-identical outputs:
+    // config 3 3976 -> 3962 us, config 5's shape 546.7 -> 542.8 us, config 2
+    // and config 5c unchanged.
+    constexpr bool LATE_Q = PIPE && DMA && CG == 1 && (D == 128 || D == 256);
+    if constexpr (!LATE_Q) {
+        load_q(qrow);
+        scale_q();
+    }
 
     f32x4 o[NOB];
 #pragma unroll
@@ -573,7 +582,20 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
             }
         }
     };
-    auto qk_stage = [&](const float* Ks, f32x4* s) {   // after qk_preload(Ks)
+    // SCALE: multiply each Q chunk by scale * log2(e) right before its
+    // MFMAs (stage 0 of LATE_Q, where Q arrives chunk by chunk); the factor
+    // passes through an empty asm there so the multiplies, and the waits for
+    // their loads, stay with their own chunk.
+    auto qk_stage = [&](const float* Ks, f32x4* s, auto scale_c) {   // after qk_preload(Ks)
+        constexpr bool SCALE = decltype(scale_c)::value;
+        auto scale_chunk = [&](int cc) {
+            if constexpr (SCALE) {
+                float cs = c;
+                asm volatile("" : "+s"(cs));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) qreg[4 * cc + i] *= cs;
+            }
+        };
         if constexpr (PRE > 0) {
             constexpr int KR = PRE + 1;
             f32x4 kk[KR][KB];
@@ -583,6 +605,7 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
                 for (int b = 0; b < KB; ++b) kk[cc][b] = kpre[cc][b];
 #pragma unroll
             for (int cc = 0; cc < NC; ++cc) {
+                scale_chunk(cc);
                 qk_mfma(kk[cc % KR], cc, s);
                 if (cc + PRE < NC) k_chunk(Ks, cc + PRE, kk[(cc + PRE) % KR]);
                 __builtin_amdgcn_sched_barrier(0);
@@ -595,6 +618,7 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
 #pragma unroll
             for (int cc = 0; cc < NC; ++cc) {
                 if (cc + 1 < NC) k_chunk(Ks, cc + 1, kk[(cc + 1) & 1]);
+                scale_chunk(cc);
                 qk_mfma(kk[cc & 1], cc, s);
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -835,12 +859,55 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
             const int rf = (gs < nA ? qb * BQ : q0_b) + 16 * tile;
             return kbase < seq_k && !(causal && kbase > rf + 15);
         };
-        // Q and K(0) first; V(0) and K(1) stream in under stage 0's QK^T.
-        if (ntot > 0) fill_stage(KL, Kh, kb_of(0), Kb0);
-        wait_vmcnt<0>();
-        __syncthreads();
-        if (ntot > 0) fill_stage(VL, Vh, kb_of(0), Vb0);
-        if (ntot > 1) fill_stage(KL, Kh, kb_of(1), Kb1);
+        if constexpr (LATE_Q) {
+            // The filling waves issue the DMA of K(0), V(0) and K(1), then
+            // every wave its Q rows as NC buffer loads (with global loads in
+            // flight next to the DMA the compiler ignores the explicit
+            // vmcnt below and waits for every load before the first LDS read;
+            // buffer loads it counts in order with the DMA).  VMEM loads of a
+            // wave complete in order, so vmcnt(N), N = the fewest loads any
+            // filling wave issues after K(0) (a partial last run still issues:
+            // some of its lanes are in range), waits for K(0) alone; the bare
+            // barrier (a workgroup fence would wait for every load) then
+            // publishes it, and stage 0's QK^T waits for each Q chunk as it
+            // uses it.
+            constexpr int RUNS_K = (SK * (LDK / 4) + 63) / 64, RUNS_V = (SK * (LDV / 4) + 63) / 64;
+            constexpr int AFTER_K0 = RUNS_V / FW + RUNS_K / FW + NC;
+            // Issued whatever ntot is (with fewer than two stages the
+            // spare fills repeat stage 0, in range and never read), so every
+            // filling wave issues the same count on one path.
+            const int kb0 = ntot > 0 ? kb_of(0) : 0, kb1 = ntot > 1 ? kb_of(1) : kb0;
+            fill_stage(KL, Kh, kb0, Kb0);
+            fill_stage(VL, Vh, kb0, Vb0);
+            fill_stage(KL, Kh, kb1, Kb1);
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("" ::: "memory");
+            {
+                // rows past seq_q and columns past d read as 0 (out of range)
+                const int rf = __builtin_amdgcn_readfirstlane(row_first);
+                const int rows = __builtin_amdgcn_readfirstlane(max(0, min(16, seq_q - rf)));
+                const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<float*>(Qh + (size_t)rf * d), (short)0, rows * d * 4, 0x00020000);
+#pragma unroll
+                for (int cc = 0; cc < NC; ++cc) {
+                    const int col = c0 + 16 * cc + 4 * g;
+                    const int off = col < d ? 4 * (li * d + col) : 0x7ffffff0;
+                    const f32x4 t = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) qreg[4 * cc + i] = t[i];
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vmcnt<AFTER_K0>();
+            asm volatile("s_barrier" ::: "memory");
+        } else {
+            // Q and K(0) first; V(0) and K(1) stream in under stage 0's QK^T.
+            if (ntot > 0) fill_stage(KL, Kh, kb_of(0), Kb0);
+            wait_vmcnt<0>();
+            __syncthreads();
+            if (ntot > 0) fill_stage(VL, Vh, kb_of(0), Vb0);
+            if (ntot > 1) fill_stage(KL, Kh, kb_of(1), Kb1);
+        }
         // Waves w and w + NW/2 share a SIMD and the lower-numbered one wins
         // MFMA issue.  With the half fill, those (non-filling) waves take
         // each stage's softmax right after its QK^T, before the barrier that
@@ -862,9 +929,12 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
         const bool sm_late = SPLIT_SM && FW < NW && fwave < 0;
         f32x4 s_cur[KB];
         bool act_cur = ntot > 0 && gstage_active(0);
+        if constexpr (LATE_Q) {
+            if (!act_cur) scale_q();
+        }
         if (act_cur) {
             qk_preload(Kb0);
-            qk_stage(Kb0, s_cur);
+            qk_stage(Kb0, s_cur, std::integral_constant<bool, LATE_Q>{});
             if constexpr (CG > 1) xs_put(s_cur, 0);   // summed and masked after the barrier
             else mask_stage(s_cur, kb_of(0));
             if (early || sm_late) softmax_part(s_cur);
@@ -931,7 +1001,7 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
                 }
                 if (switch_now) do_switch();
                 if (act_nxt) {
-                    qk_stage(k_next, s_cur);
+                    qk_stage(k_next, s_cur, std::false_type{});
                     mask_stage(s_cur, kb_of(gs + 1));
                     softmax_part(s_cur);
                 }
@@ -955,7 +1025,7 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
                 }
                 if (switch_now) do_switch();
                 if (act_nxt) {
-                    qk_stage(k_next, s_cur);
+                    qk_stage(k_next, s_cur, std::false_type{});
                     if constexpr (CG > 1) xs_put(s_cur, 1 - P);
                     else mask_stage(s_cur, kb_of(gs + 1));
                     if (sm_late) softmax_part(s_cur);
@@ -994,7 +1064,7 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
             f32x4 s[KB];
             if (act) {
                 qk_preload(Kb0);
-                qk_stage(Kb0, s);
+                qk_stage(Kb0, s, std::false_type{});
                 xs_put(s, 0);
             }
             wait_vmcnt<0>();
@@ -1041,7 +1111,7 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
             const bool act = stage_active(st);
             f32x4 s[KB];
             if (act) {
-                qk_stage(Kb0, s);
+                qk_stage(Kb0, s, std::false_type{});
                 xs_put(s, 0);
             }
             __syncthreads();   // K reads done, partial scores visible
@@ -1084,7 +1154,7 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
             if (act) {
                 qk_preload(Kb0);
                 pv_preload(Vb0);
-                qk_stage(Kb0, s);
+                qk_stage(Kb0, s, std::false_type{});
                 if constexpr (CG > 1) xs_put(s, 0);
             }
             if constexpr (CG > 1) __syncthreads();   // the tile's partial scores are in LDS
