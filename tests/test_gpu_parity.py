@@ -753,6 +753,32 @@ def test_two_block_workgroups_match_oracle():
     assert "two_blocks" not in fa.describe_launch(3, 1, 256, 200, 300, 64, True)
 
 
+def test_v3_first_stage_edges_match_oracle():
+    """v3's DMA kernels at D = 128 and 256 load Q after the first stages'
+    DMA (buffer loads; rows past seq_q and columns past d read as zeros) and
+    always issue K(0), V(0) and K(1), repeating stage 0 when there is no
+    second stage.  Key ranges of one stage and of one key, ragged query
+    tiles, padded columns, unsplit and key-split segments (which start
+    mid-range), against the oracle's CPU v2."""
+    rng = np.random.default_rng(93)
+    for d in (100, 128, 200, 256):
+        D = 128 if d <= 128 else 256
+        for sq, sk in ((70, 1), (70, 5), (70, 64), (130, 65), (16, 64), (150, 200)):
+            bh = 2
+            q = rng.standard_normal(bh * sq * d, dtype=np.float32)
+            k = rng.standard_normal(bh * sk * d, dtype=np.float32)
+            v = rng.standard_normal(bh * sk * d, dtype=np.float32)
+            for causal in (False, True):
+                want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+                for splits in (1, 2):
+                    plan = fa.describe_launch(3, 1, bh, sq, sk, d, causal, fa.PATH_PREFILL, splits)
+                    tag = f"v3 first stage {bh},{sq},{sk},{d},{causal} splits={splits}: {plan}"
+                    print("[case]", tag, flush=True)
+                    assert plan.startswith(f"fa_prefill_v3_d{D}_2"), tag
+                    got = _device_run(3, q, k, v, bh, sq, sk, d, causal, fa.PATH_PREFILL, splits, guard=64)
+                    assert_parity(got, want, tag)
+
+
 def test_reference_moves_mid_sequence():
     """Keys 0..63 with tiny logits (std 0.05) and later keys with large ones
     (std 2.4): a row's maximum jumps past the lazy 2^8 threshold after the
