@@ -435,6 +435,22 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
         // splits beats several rounds of short ones.  The grid lists only
         // workgroups with keys.
         size_t per = 0;
+        // The prefill splits' merge: the f32 split kernels at D = 64, 128,
+        // 256 write their partial tiles in register order, merged a
+        // workgroup per 16-row tile (a wave per 64 columns); the others
+        // (D = 32, column groups, 16-bit) by rows, a wave per row.
+        auto prefill_merge = [&]() {
+            if (!lp && (D == 64 || D == 128 || D == 256)) {
+                std::snprintf(buf, sizeof(buf), "fa_merge_tiles_d%d", D);
+                plan->second.gx = static_cast<unsigned>(nqt * bh);
+                plan->second.bx = static_cast<unsigned>(D);
+            } else {
+                std::snprintf(buf, sizeof(buf), "fa_merge_d%d", D);
+                plan->second.gx = static_cast<unsigned>((bh * sq + FA_MERGE_ROWS - 1) / FA_MERGE_ROWS);   // a wave per row
+                plan->second.bx = 64 * FA_MERGE_ROWS;
+            }
+            plan->second.name = buf;
+        };
         {
             const size_t SKs = (size_t)(lp ? fa_lp_stage_keys() : fa_prefill_stage_keys(D, variant));
             auto block_stages = [&](size_t b) {
@@ -529,10 +545,7 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
                 p.stream_per = static_cast<long long>(s_per);
                 p.stream_head_units = static_cast<long long>(s_uhead);
                 plan->first.gx = static_cast<unsigned>(s_wgs);
-                std::snprintf(buf, sizeof(buf), "fa_merge_d%d", D);
-                plan->second.name = buf;
-                plan->second.gx = static_cast<unsigned>((bh * sq + FA_MERGE_ROWS - 1) / FA_MERGE_ROWS);   // a wave per row
-                plan->second.bx = 64 * FA_MERGE_ROWS;
+                prefill_merge();
                 plan->ws_floats = (s_wgs + bh * nqb - 1) * (rows / 16) * (16 * (size_t)D + 32);
                 return FA_OK;
             }
@@ -563,10 +576,7 @@ int make_plan(int variant, const void* q, const void* k, const void* v, const fl
                     wgs += (causal_skip ? nqb - std::min(nqb, y * per * SKs / rows) : nqb) * bh;
                 if (wgs > imax) return FA_ERR_UNSUPPORTED;
                 plan->first.gx = static_cast<unsigned>(wgs);
-                std::snprintf(buf, sizeof(buf), "fa_merge_d%d", D);
-                plan->second.name = buf;
-                plan->second.gx = static_cast<unsigned>((bh * sq + FA_MERGE_ROWS - 1) / FA_MERGE_ROWS);   // a wave per row
-                plan->second.bx = 64 * FA_MERGE_ROWS;
+                prefill_merge();
                 plan->ws_floats = bh * nqt * nks * (16 * (size_t)D + 32);
             }
         }

@@ -1192,6 +1192,23 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
             pml[li] = m;
             pml[16 + li] = lt;
         }
+        if constexpr (VW == 4 && CG == 1) {
+            // D = 64, 128, 256: the tile in register order, each store a
+            // contiguous 1 KB (64 lanes x 16 B): f32x4 (hh * 4 + r) * 64 +
+            // lane holds columns 64 hh + 4 (4 g + r) .. + 3 of row li
+            // (fa_merge_tiles reads this order).  Stored by rows instead,
+            // every instruction wrote 16-byte pieces spread over 16 rows:
+            // measured on config 5c (v3), 106.5 -> 101.1 us for the stream
+            // split kernel with the merge.
+            f32x4* pov = reinterpret_cast<f32x4*>(po);
+#pragma unroll
+            for (int hh = 0; hh < NVR; ++hh)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    pov[(hh * 4 + r) * 64 + lane] =
+                        (f32x4){o[4 * hh][r], o[4 * hh + 1][r], o[4 * hh + 2][r], o[4 * hh + 3][r]};
+            return;
+        }
 #pragma unroll
         for (int hh = 0; hh < NVR; ++hh)
 #pragma unroll
@@ -1855,6 +1872,75 @@ __device__ __forceinline__ void merge_body(const FaParams& p) {
         if (4 * ch + e < p.d) orow[4 * ch + e] = acc[e] * inv;
 }
 
+// fa_merge_tiles: the log-sum-exp merge of the f32 prefill key split and
+// stream split at D = 64, 128, 256, whose partials are 16-row tiles in
+// register order (prefill_segment: f32x4 (hh * 4 + r) * 64 + lane holds
+// columns 64 hh + 4 (4 g + r) .. + 3 of row li = lane % 16, g = lane / 16).
+// One workgroup per (slice, 16-row tile), one wave per 64-column group hh:
+// every load is a contiguous 1 KB, and each lane keeps the columns it
+// stores.  The splits of a tile, their slots and the weights 2^((m - M) c)
+// are those of merge_body, taken row by row in each lane.
+template <int D>
+__device__ __forceinline__ void merge_tiles_body(const FaParams& p) {
+    static_assert(D == 64 || D == 128 || D == 256, "register-order tiles: D = 64, 128, 256");
+    const int lane = threadIdx.x & 63;
+    const int hh = threadIdx.x >> 6;    // the wave's 64-column group
+    const int li = lane & 15, g = lane >> 4;
+    const int bh = blockIdx.x / p.nqt, qt = blockIdx.x % p.nqt;
+    if (bh >= p.bh) return;
+    const int q0 = 16 * qt;
+    const float c = p.merge_scale;
+    size_t pbase = ((size_t)bh * p.nqt + qt) * p.num_splits, pstride = 1;
+    int ns = p.num_splits;
+    if (p.stream_per > 0) {
+        const StreamGeom sg = stream_geom(p, p.ks_rows, p.split_len);
+        const int blk = q0 / p.ks_rows;
+        unsigned first, last;
+        stream_span(sg, (unsigned)p.stream_per, (unsigned)bh, (unsigned)blk, first, last);
+        if (first == last) return;   // one workgroup wrote the block's rows
+        ns = (int)(last - first + 1);
+        pstride = (size_t)(p.ks_rows / 16);
+        pbase = ((size_t)first + (size_t)bh * p.nqb + blk) * pstride + (q0 % p.ks_rows) / 16;
+    } else {
+        const int kend = (p.causal && !p.full_keys) ? min(p.seq_k, (q0 / p.ks_rows + 1) * p.ks_rows) : p.seq_k;
+        ns = min(ns, (kend + p.split_len - 1) / p.split_len);
+    }
+    float M = FA_NEG_INF;
+    for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, p.part_ml[(pbase + sp * pstride) * 32 + li]);
+    const float Mu = (M == FA_NEG_INF) ? 0.0f : M;
+    float L = 0.0f;
+    f32x4 acc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 2
+    for (int sp = 0; sp < ns; ++sp) {
+        const size_t slot = pbase + sp * pstride;
+        const float* ml = p.part_ml + slot * 32;
+        const float w = rescale_factor(ml[li], Mu, c);
+        L += ml[16 + li] * w;
+        const f32x4* po = reinterpret_cast<const f32x4*>(p.part_o + slot * 16 * D) + hh * 4 * 64 + lane;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] += po[r * 64] * w;
+    }
+    const int row = q0 + li;
+    if (row >= p.seq_q) return;
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    float* orow = p.out + ((size_t)bh * p.seq_q + row) * p.d;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int dv0 = 64 * hh + 4 * (4 * g + r);
+        // 128-bit stores where the output allows them (the split kernels
+        // also serve unaligned outputs and d % 4 != 0 through scalar loads)
+        if (dv0 + 4 <= p.d && (reinterpret_cast<uintptr_t>(orow + dv0) & 15) == 0) {
+            *reinterpret_cast<f32x4*>(orow + dv0) = acc[r] * inv;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (dv0 + e < p.d) orow[dv0 + e] = acc[r][e] * inv;
+        }
+    }
+}
+
 #include "fa_decode_rows.inc"
 
 // ---------------------------------------------------------------------------
@@ -2429,6 +2515,12 @@ FA_DECODE_ROWS_LP_ALL(f16, _Float16)
 
 #define FA_MERGE(D) \
     extern "C" __global__ void __launch_bounds__(64 * FA_MERGE_ROWS) fa_merge_d##D(FaParams p) { merge_body<D>(p); }
+// fa_merge_tiles_d{D}: the f32 prefill splits' merge (register-order tiles)
+#define FA_MERGE_TILES(D) \
+    extern "C" __global__ void __launch_bounds__(D) fa_merge_tiles_d##D(FaParams p) { merge_tiles_body<D>(p); }
+FA_MERGE_TILES(64)
+FA_MERGE_TILES(128)
+FA_MERGE_TILES(256)
 FA_MERGE(32)
 FA_MERGE(64)
 FA_MERGE(128)

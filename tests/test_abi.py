@@ -263,7 +263,8 @@ def test_planning_stream_split_prefill():
     # 4592 in all -> runs of 18 over 256 workgroups; block slots = 256 + 128 - 1
     # of 8 tiles x (16 x 256 + 32) floats
     s = describe(3, 1, 16, 1000, 1000, 256, True)
-    assert s.startswith("fa_prefill_v3_d256_2s grid=256x1x1 block=512; fa_merge_d256 grid=4000x1x1 block=256; ")
+    # merged a workgroup per 16-row tile (16 slices x 63 tiles), a wave per 64 columns
+    assert s.startswith("fa_prefill_v3_d256_2s grid=256x1x1 block=512; fa_merge_tiles_d256 grid=1008x1x1 block=256; ")
     assert "stream_per=18" in s and f"workspace={(256 + 128 - 1) * 8 * (16 * 256 + 32) * 4}" in s
     # v2's 32-key stages: 4 + 8 + ... + 28 + 32 = 144 per head -> runs of 9
     assert "grid=256x1x1" in describe(2, 1, 16, 1000, 1000, 256, True) and \
@@ -295,7 +296,7 @@ def test_planning_stream_split_refuses_unit_totals_past_32_bits():
 def test_planning_key_split_prefill():
     # config 5c's shape, split forced over 3 workgroups per block
     s = describe(3, 1, 16, 1000, 1000, 256, True, fa.PATH_PREFILL, 3)
-    assert s.startswith("fa_prefill_v3_d256_2s grid=") and "fa_merge_d256 grid=4000x1x1" in s   # split instantiation
+    assert s.startswith("fa_prefill_v3_d256_2s grid=") and "fa_merge_tiles_d256 grid=1008x1x1" in s   # split instantiation
     assert "stream_per" not in s
     nks, split_len = int(s.split("splits=")[1].split()[0]), int(s.split("split_len=")[1].split()[0])
     assert split_len % 16 == 0 and nks * split_len >= 1000 > (nks - 1) * split_len
@@ -304,7 +305,7 @@ def test_planning_key_split_prefill():
     assert f"grid={wgs}x1x1" in s
     # v1 (config 5c): every block visits all 1000 keys = 32 stages of 32; two splits of 16 stages
     s = describe(1, 1, 16, 1000, 1000, 256, True)
-    assert s.startswith("fa_prefill_v1_d256_1s grid=256x1x1 block=512; fa_merge_d256 grid=4000x1x1 ")
+    assert s.startswith("fa_prefill_v1_d256_1s grid=256x1x1 block=512; fa_merge_tiles_d256 grid=1008x1x1 ")
     assert "splits=2 split_len=512" in s and "stream_per" not in s
     s = describe(1, 1, 16, 1000, 1000, 256, True, fa.PATH_PREFILL, 3)   # forced: all 8 blocks in every split
     assert s.startswith("fa_prefill_v1_d256_1s grid=384x1x1") and "splits=3 split_len=352" in s
@@ -313,6 +314,12 @@ def test_planning_key_split_prefill():
     assert "fa_merge" not in describe(3, 1, 32, 2048, 2048, 128, True)    # full grid
     s = describe(2, 1, 1, 300, 700, 64, False, fa.PATH_PREFILL, 3)   # 11 stages of 64 keys -> 4 per split
     assert s.startswith("fa_prefill_v2_d64_1s grid=9x1x1") and "splits=3 split_len=256" in s
+    assert "fa_merge_tiles_d64 grid=19x1x1 block=64" in s   # 19 tiles of 16 rows, one wave each
+    # register-order partials at D = 64, 128, 256 only: D = 32 and 16-bit inputs merge by rows
+    assert "fa_merge_d32 grid=75x1x1 block=256" in describe(2, 1, 1, 300, 700, 32, False, fa.PATH_PREFILL, 3)
+    assert "fa_merge_tiles_d128 grid=19x1x1 block=128" in describe(3, 1, 1, 300, 700, 128, False, fa.PATH_PREFILL, 3)
+    assert "fa_merge_d128 grid=75x1x1" in describe(3, 1, 1, 300, 700, 128, False, fa.PATH_PREFILL, 3,
+                                                    dtype=fa.DTYPE_BF16)
     assert "splits=6 split_len=128" in describe(3, 1, 1, 300, 700, 64, False, fa.PATH_PREFILL, 6)
 
 
