@@ -804,11 +804,71 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
 
     // Final normalisation with the l > 0 guard (src/v2.rs:375-382; v1's
     // accumulator is already normalised, src/v1.rs:389-393).
+    // The O chunks this lane stores for column group hh, scaled by inv, in
+    // row order: a 4 x 4 transpose over (lane group g, register r) by two
+    // permlane-swap levels turns "columns 64 hh + 4 (4 g + r)" into "columns
+    // 64 hh + 16 r + 4 g", so each store instruction writes 64 contiguous
+    // bytes of every row instead of 16-byte pieces 64 bytes apart.
+    auto row_chunks = [&](int hh, float inv, f32x4* x) {
+        float v[4][4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[r][e] = o[4 * hh + e][r] * inv;
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[r][e]), __float_as_uint(v[r + 2][e]),
+                                                                false, false);
+                v[r][e] = __uint_as_float(t[0]);
+                v[r + 2][e] = __uint_as_float(t[1]);
+            }
+#pragma unroll
+        for (int r = 0; r < 4; r += 2)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[r][e]), __float_as_uint(v[r + 1][e]),
+                                                                false, false);
+                v[r][e] = __uint_as_float(t[0]);
+                v[r + 1][e] = __uint_as_float(t[1]);
+            }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[r] = (f32x4){v[r][0], v[r][1], v[r][2], v[r][3]};
+    };
+    // Row-order stores where measured faster (MI355X, bit-identical): config 5
+    // v1 / v2 / v3 610.3 / 570.7 / 543.2 -> 602.3 / 559.7 / 536.4 us, config 2
+    // v1 / v2 559.6 / 288.0 -> 557.5 / 285.7 us.  Not for the v3 D = 128
+    // kernel (config 3 3965 -> 4001 us) nor the split kernels (config 5c
+    // 0.2-1.0 us slower), which keep the register-order stores below.
+    constexpr bool ROW_STORES = VW == 4 && !(VARIANT == 3 && D == 128) && !STREAM;
     auto write_out = [&]() {
         float inv = 1.0f;
         if (VARIANT != 1) {
             const float lt = row4_sum(l);
             inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        }
+        if constexpr (ROW_STORES) {
+            float* orow = Oh + (size_t)qrow * d;
+#pragma unroll
+            for (int hh = 0; hh < NVR; ++hh) {
+                f32x4 x[4];
+                row_chunks(hh, inv, x);   // every lane takes part in the swaps
+                if (qrow < seq_q) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const int dv0 = c0 + 64 * hh + 16 * k + 4 * g;
+                        if (LOADER != 0 && dv0 + 4 <= d) {
+                            *reinterpret_cast<f32x4*>(orow + dv0) = x[k];
+                        } else {
+#pragma unroll
+                            for (int j = 0; j < 4; ++j)
+                                if (dv0 + j < d) orow[dv0 + j] = x[k][j];
+                        }
+                    }
+                }
+            }
+            return;
         }
         if (qrow < seq_q) {
             float* orow = Oh + (size_t)qrow * d;
