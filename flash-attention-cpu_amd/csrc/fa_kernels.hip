@@ -288,6 +288,32 @@ __device__ __forceinline__ float row4_sum(float x) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// 4 x 4 transpose over (16-lane group g, register r) of four f32x4 values:
+// afterwards v[r] of lane group g holds what v[g] of lane group r held.  Two
+// permlane-swap levels (halves, then 16-lane rows), as in row4_max.  Used to
+// turn an O^T tile's "columns 64 hh + 4 (4 g + r)" into "columns 64 hh + 16 r
+// + 4 g", so a store instruction writes 64 contiguous bytes of every row.
+__device__ __forceinline__ void lane_group_transpose4(float (&v)[4][4]) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[r][e]), __float_as_uint(v[r + 2][e]),
+                                                            false, false);
+            v[r][e] = __uint_as_float(t[0]);
+            v[r + 2][e] = __uint_as_float(t[1]);
+        }
+#pragma unroll
+    for (int r = 0; r < 4; r += 2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[r][e]), __float_as_uint(v[r + 1][e]),
+                                                            false, false);
+            v[r][e] = __uint_as_float(t[0]);
+            v[r + 1][e] = __uint_as_float(t[1]);
+        }
+}
+
 // One workgroup's share of a query block: query block qb of slice bh (and,
 // in the two-block grid, block qb_second after it), key stages sbeg ..
 // sbeg + nst - 1 of the block's range (nst < 0: to its end); slot >= 0
@@ -805,34 +831,16 @@ __device__ __forceinline__ void prefill_segment(const FaParams& p, const Prefill
     // Final normalisation with the l > 0 guard (src/v2.rs:375-382; v1's
     // accumulator is already normalised, src/v1.rs:389-393).
     // The O chunks this lane stores for column group hh, scaled by inv, in
-    // row order: a 4 x 4 transpose over (lane group g, register r) by two
-    // permlane-swap levels turns "columns 64 hh + 4 (4 g + r)" into "columns
-    // 64 hh + 16 r + 4 g", so each store instruction writes 64 contiguous
-    // bytes of every row instead of 16-byte pieces 64 bytes apart.
+    // row order (lane_group_transpose4): each store instruction then writes
+    // 64 contiguous bytes of every row instead of 16-byte pieces 64 bytes
+    // apart.
     auto row_chunks = [&](int hh, float inv, f32x4* x) {
         float v[4][4];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[r][e] = o[4 * hh + e][r] * inv;
-#pragma unroll
-        for (int r = 0; r < 2; ++r)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[r][e]), __float_as_uint(v[r + 2][e]),
-                                                                false, false);
-                v[r][e] = __uint_as_float(t[0]);
-                v[r + 2][e] = __uint_as_float(t[1]);
-            }
-#pragma unroll
-        for (int r = 0; r < 4; r += 2)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[r][e]), __float_as_uint(v[r + 1][e]),
-                                                                false, false);
-                v[r][e] = __uint_as_float(t[0]);
-                v[r + 1][e] = __uint_as_float(t[1]);
-            }
+        lane_group_transpose4(v);
 #pragma unroll
         for (int r = 0; r < 4; ++r) x[r] = (f32x4){v[r][0], v[r][1], v[r][2], v[r][3]};
     };
@@ -1937,8 +1945,8 @@ __device__ __forceinline__ void merge_body(const FaParams& p) {
 // register order (prefill_segment: f32x4 (hh * 4 + r) * 64 + lane holds
 // columns 64 hh + 4 (4 g + r) .. + 3 of row li = lane % 16, g = lane / 16).
 // One workgroup per (slice, 16-row tile), one wave per 64-column group hh:
-// every load is a contiguous 1 KB, and each lane keeps the columns it
-// stores.  The splits of a tile, their slots and the weights 2^((m - M) c)
+// every load is a contiguous 1 KB, and the rows are stored 64 contiguous
+// bytes at a time (lane_group_transpose4).  The splits of a tile, their slots and the weights 2^((m - M) c)
 // are those of merge_body, taken row by row in each lane.
 template <int D>
 __device__ __forceinline__ void merge_tiles_body(const FaParams& p) {
@@ -1983,20 +1991,30 @@ __device__ __forceinline__ void merge_tiles_body(const FaParams& p) {
         for (int r = 0; r < 4; ++r) acc[r] += po[r * 64] * w;
     }
     const int row = q0 + li;
-    if (row >= p.seq_q) return;
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    // row order (every lane takes part in the swaps): columns 64 hh + 16 r +
+    // 4 g, 64 contiguous bytes of every row per store (config 5c: ~0.3 us)
+    float v[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[r][e] = acc[r][e] * inv;
+    lane_group_transpose4(v);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = (f32x4){v[r][0], v[r][1], v[r][2], v[r][3]};
+    if (row >= p.seq_q) return;
     float* orow = p.out + ((size_t)bh * p.seq_q + row) * p.d;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const int dv0 = 64 * hh + 4 * (4 * g + r);
+        const int dv0 = 64 * hh + 16 * r + 4 * g;
         // 128-bit stores where the output allows them (the split kernels
         // also serve unaligned outputs and d % 4 != 0 through scalar loads)
         if (dv0 + 4 <= p.d && (reinterpret_cast<uintptr_t>(orow + dv0) & 15) == 0) {
-            *reinterpret_cast<f32x4*>(orow + dv0) = acc[r] * inv;
+            *reinterpret_cast<f32x4*>(orow + dv0) = acc[r];
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                if (dv0 + e < p.d) orow[dv0 + e] = acc[r][e] * inv;
+                if (dv0 + e < p.d) orow[dv0 + e] = acc[r][e];
         }
     }
 }
