@@ -333,7 +333,7 @@ def main() -> int:
                 result_head = (wl, kernels, ms_step, ms_kernel)
                 log(f"[bench] {name} v{var}: {ms_step * 1e3:.1f} us/step wall, {ms_kernel * 1e3:.1f} us kernel")
                 if not args.quick:
-                    # The survey's protocol: R = 5 repeats of 20 launches, median us/call.
+                    # Repeat protocol: R = 5 repeats of 20 launches, median us/call.
                     reps = sorted(time_calls(torch, call, 20, 3)[1] for _ in range(5))
                     entry[f"v{var}_median_5x20_us"] = round(reps[2] * 1e3, 1)
             else:
