@@ -23,9 +23,14 @@ parity reference: every GPU output timed here is compared with it (max-abs,
 relative L2; north_star bar 2e-5 / 1e-5), and the headline's figures are the
 top-level ``parity`` object.
 
+Before the configurations, peak probes (fa_probe_launch: back-to-back f32 and
+bf16 MFMA streams on every CU, a 1 GiB device copy) measure the ceilings the
+data-sheet peaks stand for on this GPU (``extra.measured_peaks``; the roofline
+itself keeps the data-sheet denominators).
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--variant 3]
                        [--quick | --configs config2,config4a,...]
-                       [--no-cpu-baseline] [--cpu-seconds S] [--csv PATH]
+                       [--no-cpu-baseline] [--no-peaks] [--cpu-seconds S] [--csv PATH]
 Prints exactly one JSON line on stdout (compact: per config and variant the
 kernel time, throughput, % of peak, counters where profiled, and parity);
 progress goes to stderr, which ends with a one-line-per-config summary.
@@ -121,6 +126,51 @@ class Workload:
 
 
 RAMP_SECONDS = 0.3   # untimed sustained work before each measurement (clock ramp)
+
+# Peak probes (fa_probe_launch): kind, label, iterations per launch (about 4 ms
+# of MFMA work each at the data-sheet rate), data-sheet peak, unit.
+PROBES = (
+    ("fp32_mfma_32x32x2", 0, 5000, PEAK_TFLOPS, "TFLOP/s"),
+    ("fp32_mfma_16x16x4", 1, 5000, PEAK_TFLOPS, "TFLOP/s"),
+    ("bf16_mfma_16x16x32", 2, 5000, PEAK_TFLOPS_16, "TFLOP/s"),
+    ("bf16_mfma_32x32x16", 4, 5000, PEAK_TFLOPS_16, "TFLOP/s"),
+    ("hbm_copy", 3, 0, PEAK_GBS, "GB/s"),
+)
+PROBE_COPY_BYTES = 2 << 30   # 1 GiB copied onto another 1 GiB
+
+
+def measure_peaks(torch, fa) -> dict:
+    """The machine's own ceilings next to the data-sheet peaks the roofline
+    divides by: back-to-back MFMA streams on every CU (FLOP per launch from
+    fa_probe_launch) and a 1 GiB device copy (bytes read + written), each the best of 5 launches after a clock ramp, timed with HIP
+    events on the launch stream."""
+    stream = torch.cuda.current_stream()
+    buf = torch.empty(PROBE_COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    out = {}
+    for label, kind, iters, peak, unit in PROBES:
+        def call():
+            return fa.probe_launch(kind, stream.cuda_stream, buf.data_ptr(), PROBE_COPY_BYTES, iters)
+        t_ramp = time.perf_counter()
+        while time.perf_counter() - t_ramp < RAMP_SECONDS:
+            call()
+            torch.cuda.synchronize()
+        best = None
+        for _ in range(5):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            work = call()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1)
+            best = ms if best is None else min(best, ms)
+        rate = work / (best * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
+        out[label] = {"value": round(rate, 1), "unit": unit, "datasheet": peak,
+                      "frac_of_datasheet": round(rate / peak, 4), "ms": round(best, 3)}
+        log(f"[bench] peak probe {label}: {rate:.1f} {unit} ({rate / peak * 100:.1f} % of the data sheet's {peak:g})")
+    del buf
+    torch.cuda.empty_cache()
+    return out
 
 
 def time_calls(torch, call, steps: int, warmup: int):
@@ -257,6 +307,7 @@ def main() -> int:
     ap.add_argument("--configs", default="",
                     help="comma-separated subset of " + ",".join(c[0] for c in CONFIGS) + " (the headline always runs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-peaks", action="store_true", help="skip the MFMA / copy peak probes")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU budget of the headline baseline")
     ap.add_argument("--cpu-seconds-other", type=float, default=2.5, help="CPU budget of each other config")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -289,6 +340,7 @@ def main() -> int:
     from flash_attention_amd import traffic as trf
 
     fa.init()
+    peaks = {} if args.no_peaks else measure_peaks(torch, fa)
     traffic_table = os.path.join(ROOT, "profiles", "traffic.json")
     pmc_table = os.path.join(ROOT, "profiles", "pmc.json")
     configs = {}
@@ -428,6 +480,10 @@ def main() -> int:
         "extra": {"configs": configs, "traffic_note": traffic_note,
                   "kernel_source_sha256": trf.kernel_source_hash()},
     }
+    if peaks:
+        # the headline kernel against the FP32 MFMA rate this GPU itself sustains
+        result["extra"]["measured_peaks"] = dict(
+            peaks, headline_frac_of_measured=round(achieved / peaks["fp32_mfma_16x16x4"]["value"], 4))
 
     if pending_cpu:
         threads = host_cores()
@@ -467,6 +523,9 @@ def main() -> int:
         append_history(args.csv, history)
     for line in summary_lines(configs):
         log(line)
+    if peaks:
+        log("[summary] peaks: " + " | ".join(f"{k} {v['value']:g} {v['unit']} ({v['frac_of_datasheet'] * 100:.1f} %)"
+                                            for k, v in peaks.items()))
     print(json.dumps(result, separators=(",", ":")), flush=True)
     return 0
 

@@ -2619,3 +2619,104 @@ FA_NAIVE(float, f32)
 FA_NAIVE(double, f64)
 
 #include "fa_lp.inc"
+
+// ---------------------------------------------------------------------------
+// Peak probes (new; no counterpart in the reference): the ceilings that the
+// roofline fractions divide by, measured on the machine itself.
+//  * fa_probe_mfma_*: every wave runs CH independent accumulator chains of
+//    `iters` back-to-back MFMAs on lane-dependent inputs, then stores one
+//    checksum; FLOP per launch = waves x iters x CH x FLOP per MFMA.  Each
+//    chain's first step is peeled off the loop (from a zero accumulator): with
+//    zero-initialised accumulators carried into it, the compiler shuffled
+//    accumulator registers inside the loop (v_accvgpr_mov, 10 % of the rate).  A 64 KiB
+//    LDS reservation holds the CU to two workgroups, two waves per SIMD as in
+//    the attention kernels (measured on MI355X: eight waves per SIMD lose
+//    10-40 % of the MFMA rate; the small bf16 MFMA needs many chains).
+//  * fa_probe_copy: a grid-stride device copy of n16 16-byte elements from the
+//    first half of the buffer to the second; bytes per launch = 2 x 16 x n16
+//    (read + write).
+// ---------------------------------------------------------------------------
+constexpr int kProbeLdsFloats = 16384;   // 64 KiB per workgroup
+
+template <int KIND>
+__device__ __forceinline__ void probe_mfma_body(const ProbeParams& p) {
+    __shared__ float hold[kProbeLdsFloats];
+    const int lane = threadIdx.x & 63;
+    const unsigned wave = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+    // the reservation is used, so it stays allocated
+    hold[threadIdx.x * (kProbeLdsFloats / 256)] = (float)lane;
+    __syncthreads();
+    const float a = 1.0f + (float)lane * 1.0e-3f, b = 1.0f - (float)lane * 1.0e-3f;
+    const unsigned iters = p.iters;
+    float sum = 0.0f;
+    if constexpr (KIND == 0) {
+        constexpr int CH = 4;
+        f32x16 acc[CH];
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch) acc[ch] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, (f32x16){}, 0, 0, 0);
+        for (unsigned it = 1; it < iters; ++it)
+#pragma unroll
+            for (int ch = 0; ch < CH; ++ch) acc[ch] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[ch], 0, 0, 0);
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) sum += acc[ch][e];
+    } else if constexpr (KIND == 1) {
+        constexpr int CH = 8;
+        f32x4 acc[CH];
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch) acc[ch] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, (f32x4){}, 0, 0, 0);
+        for (unsigned it = 1; it < iters; ++it)
+#pragma unroll
+            for (int ch = 0; ch < CH; ++ch) acc[ch] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[ch], 0, 0, 0);
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sum += acc[ch][e];
+    } else {
+        // KIND 2: v_mfma_f32_16x16x32_bf16, 16 chains; KIND 4: v_mfma_f32_32x32x16_bf16, 4 chains
+        constexpr bool BIG = KIND == 4;
+        constexpr int CH = BIG ? 4 : 16;
+        typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+        bf16x8 va, vb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            va[e] = (__bf16)(a + (float)e * 1.0e-2f);
+            vb[e] = (__bf16)(b - (float)e * 1.0e-2f);
+        }
+        typedef typename std::conditional<BIG, f32x16, f32x4>::type acc_t;
+        constexpr int NE = BIG ? 16 : 4;
+        acc_t acc[CH];
+        auto step = [&](acc_t c) -> acc_t {
+            if constexpr (BIG) return __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, vb, c, 0, 0, 0);
+            else return __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, vb, c, 0, 0, 0);
+        };
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch) acc[ch] = step((acc_t){});
+        for (unsigned it = 1; it < iters; ++it)
+#pragma unroll
+            for (int ch = 0; ch < CH; ++ch) acc[ch] = step(acc[ch]);
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch)
+#pragma unroll
+            for (int e = 0; e < NE; ++e) sum += acc[ch][e];
+    }
+    // read after the chains, so nothing but the accumulators is live across them
+    sum += hold[(255 - threadIdx.x) * (kProbeLdsFloats / 256)] * 0.0f;
+    if (lane == 0) p.buf[wave] = sum;
+}
+
+__device__ __forceinline__ void probe_copy_body(const ProbeParams& p) {
+    const f32x4* __restrict__ src = reinterpret_cast<const f32x4*>(p.buf);
+    f32x4* __restrict__ dst = reinterpret_cast<f32x4*>(p.buf) + p.n16;
+    const unsigned long long n = p.n16;
+    const unsigned long long stride = (unsigned long long)gridDim.x * blockDim.x;
+    for (unsigned long long i = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        dst[i] = src[i];
+}
+
+extern "C" __global__ void __launch_bounds__(256) fa_probe_mfma_f32_32x32x2(ProbeParams p) { probe_mfma_body<0>(p); }
+extern "C" __global__ void __launch_bounds__(256) fa_probe_mfma_f32_16x16x4(ProbeParams p) { probe_mfma_body<1>(p); }
+extern "C" __global__ void __launch_bounds__(256) fa_probe_mfma_bf16_16x16x32(ProbeParams p) { probe_mfma_body<2>(p); }
+extern "C" __global__ void __launch_bounds__(256) fa_probe_copy(ProbeParams p) { probe_copy_body(p); }
+extern "C" __global__ void __launch_bounds__(256) fa_probe_mfma_bf16_32x32x16(ProbeParams p) { probe_mfma_body<4>(p); }

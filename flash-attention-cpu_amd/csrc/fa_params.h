@@ -55,6 +55,14 @@ typedef struct NaiveParams {
     double scale_d;      // 1/sqrt(d) in f64 (f64 instantiation)
 } NaiveParams;
 
+// Peak probes (fa_probe_mfma_*, fa_probe_copy): the machine's own ceilings
+// for the roofline denominators.
+typedef struct ProbeParams {
+    float* buf;                 // MFMA probes: one checksum per wave; copy: source half, then destination half
+    unsigned long long n16;     // copy: 16-byte elements per half
+    unsigned iters;             // MFMA probes: iterations of the independent MFMA chains
+} ProbeParams;
+
 
 // Prefill geometry shared by the host planner and the kernels: waves per
 // workgroup (each wave owns 16 query rows) and keys per LDS stage.

@@ -69,7 +69,7 @@ EXPORTED_SYMBOLS = (
     "fa_device_ex", "fa_device_ex_noalloc",
     "fa_device_lp", "fa_multihead_lp",
     "fa_naive_attention", "fa_naive_device",
-    "fa_init", "fa_describe_launch",
+    "fa_init", "fa_describe_launch", "fa_probe_launch",
 )
 
 
@@ -174,6 +174,9 @@ def lib() -> ctypes.CDLL:
     L.fa_describe_launch.argtypes = [ctypes.c_int, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_int, _OPTS,
                                      ctypes.c_char_p, _SZ]
     L.fa_describe_launch.restype = ctypes.c_int
+    L.fa_probe_launch.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, _SZ, ctypes.c_uint,
+                                  ctypes.POINTER(ctypes.c_double)]
+    L.fa_probe_launch.restype = ctypes.c_int
     _lib = L
     return L
 
@@ -381,6 +384,23 @@ def describe_launch(variant: int, batch: int, heads: int, seq_len_q: int, seq_le
     _check(lib().fa_describe_launch(int(variant), batch, heads, seq_len_q, seq_len_k, d_head,
                                     1 if causal else 0, ctypes.byref(opts), buf, len(buf)))
     return buf.value.decode()
+
+
+PROBE_MFMA_F32_32X32X2 = 0
+PROBE_MFMA_F32_16X16X4 = 1
+PROBE_MFMA_BF16_16X16X32 = 2
+PROBE_COPY = 3
+PROBE_MFMA_BF16_32X32X16 = 4
+
+
+def probe_launch(kind: int, stream: int, buf: int, nbytes: int, iters: int = 0) -> float:
+    """Queue one peak-probe kernel (fa_probe_launch) on `stream` over device
+    memory `buf` (`nbytes` long); returns its work: FLOP for the MFMA probes,
+    bytes read + written for the copy.  The caller times it."""
+    work = ctypes.c_double(0.0)
+    _check(lib().fa_probe_launch(int(kind), ctypes.c_void_p(stream), ctypes.c_void_p(buf), int(nbytes),
+                                 int(iters), ctypes.byref(work)))
+    return work.value
 
 
 def init() -> None:

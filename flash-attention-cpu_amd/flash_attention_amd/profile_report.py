@@ -195,7 +195,8 @@ def trace_markdown(run_dir: str, calls, src: str) -> str:
         "|---|---|---|---|---|---|---|",
     ]
     for (name, grid), r in rows:
-        lines.append(f"| {name} | {grid} | {', '.join(users.get((name, grid), ['(other)']))} | {r['calls']} | "
+        other = ["peak probe (bench.py measure_peaks)"] if name.startswith("fa_probe_") else ["(other)"]
+        lines.append(f"| {name} | {grid} | {', '.join(users.get((name, grid), other))} | {r['calls']} | "
                      f"{r['avg_us']:.1f} | {r['min_us']:.1f} | {r['max_us']:.1f} |")
     return "\n".join(lines) + "\n"
 

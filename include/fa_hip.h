@@ -277,6 +277,25 @@ int fa_describe_launch(int variant, size_t batch, size_t heads, size_t seq_len_q
                        size_t d_head, int causal, const fa_launch_opts* opts, char* buf,
                        size_t buf_len);
 
+/* ---- peak probes ---------------------------------------------------------
+ * No counterpart in the reference: a measurement aid, so the roofline
+ * denominators (the MI355X data-sheet peaks) can be checked against the
+ * machine.  Queues one probe kernel on `stream` (device memory `buf`, 16-byte
+ * aligned, `bytes` long) and stores its work in *work; the caller times it.
+ *   FA_PROBE_MFMA_*: every wave of 8 x #CUs four-wave workgroups (two
+ *     resident per CU) runs independent chains of `iters` back-to-back MFMAs
+ *     of that kind and writes one checksum float to buf (bytes >= 128 x #CUs);
+ *     *work = FLOP.
+ *   FA_PROBE_COPY: copies the first bytes/2 of buf (whole 16-byte elements)
+ *     onto the second half;
+ *     *work = bytes read + bytes written. */
+#define FA_PROBE_MFMA_F32_32X32X2 0
+#define FA_PROBE_MFMA_F32_16X16X4 1
+#define FA_PROBE_MFMA_BF16_16X16X32 2
+#define FA_PROBE_COPY 3
+#define FA_PROBE_MFMA_BF16_32X32X16 4
+int fa_probe_launch(int kind, void* stream, void* buf, size_t bytes, unsigned iters, double* work);
+
 #ifdef __cplusplus
 }
 #endif
