@@ -340,7 +340,14 @@ def main() -> int:
     from flash_attention_amd import traffic as trf
 
     fa.init()
-    peaks = {} if args.no_peaks else measure_peaks(torch, fa)
+    peaks, peaks_error = {}, None
+    if not args.no_peaks:
+        try:   # a measurement aid: a failure here must not cost the benchmark line
+            peaks = measure_peaks(torch, fa)
+        except (RuntimeError, fa.FaError) as e:
+            peaks_error = f"{type(e).__name__}: {e}"
+            log(f"[bench] peak probes skipped: {peaks_error}")
+            torch.cuda.empty_cache()
     traffic_table = os.path.join(ROOT, "profiles", "traffic.json")
     pmc_table = os.path.join(ROOT, "profiles", "pmc.json")
     configs = {}
@@ -480,6 +487,8 @@ def main() -> int:
         "extra": {"configs": configs, "traffic_note": traffic_note,
                   "kernel_source_sha256": trf.kernel_source_hash()},
     }
+    if peaks_error:
+        result["extra"]["measured_peaks"] = {"error": peaks_error}
     if peaks:
         # the headline kernel against the FP32 MFMA rate this GPU itself sustains
         result["extra"]["measured_peaks"] = dict(
