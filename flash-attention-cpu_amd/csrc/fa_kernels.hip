@@ -2630,8 +2630,7 @@ FA_NAIVE(double, f64)
 //    zero-initialised accumulators carried into it, the compiler shuffled
 //    accumulator registers inside the loop (v_accvgpr_mov, 10 % of the rate).  A 64 KiB
 //    LDS reservation holds the CU to two workgroups, two waves per SIMD as in
-//    the attention kernels (measured on MI355X: eight waves per SIMD lose
-//    10-40 % of the MFMA rate; the small bf16 MFMA needs many chains).
+//    the attention kernels.
 //  * fa_probe_copy: a grid-stride device copy of n16 16-byte elements from the
 //    first half of the buffer to the second; bytes per launch = 2 x 16 x n16
 //    (read + write).
