@@ -727,6 +727,41 @@ def test_stream_split_prefill_matches_oracle():
     assert "stream_per=18" in fa.describe_launch(3, 1, 16, 1000, 1000, 256, True)   # config 5c: automatic
 
 
+def test_misaligned_device_pointers_match_oracle():
+    """Device pointers 4 bytes past a 16-byte boundary (Q, K, V and out each
+    offset by one float, d % 4 == 0): the planner takes the scalar loaders and
+    the merges' element-wise stores; every path (automatic, prefill, key split,
+    stream split, split-KV tiles) and variant against the oracle, with
+    sentinels around out."""
+    torch = _torch()
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(83)
+    cases = [(1, 1000, 1000, 256, True), (3, 300, 700, 64, False), (2, 200, 200, 128, True),
+             (4, 1, 2048, 128, False), (2, 16, 1500, 64, False), (1, 256, 256, 64, False)]
+    for bh, sq, sk, d, causal in cases:
+        q = rng.standard_normal(bh * sq * d, dtype=np.float32)
+        k = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        v = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        want = cpu_v2(q, k, v, bh, sq, sk, d, causal)
+        tq, tk, tv = (torch.from_numpy(np.concatenate([np.zeros(1, np.float32), x])).to(dev) for x in (q, k, v))
+        for path, splits in ((fa.PATH_AUTO, 0), (fa.PATH_PREFILL, 0), (fa.PATH_PREFILL, 3), (fa.PATH_STREAM, 0),
+                             (fa.PATH_SPLITKV, 2)):
+            for variant in ALL_VARIANTS:
+                # (describe_launch plans for aligned pointers; these calls take the scalar loaders)
+                tag = (f"misaligned v{variant} path={path} splits={splits} {bh},{sq},{sk},{d},{causal}; aligned plan: "
+                       f"{fa.describe_launch(variant, 1, bh, sq, sk, d, causal, path, splits)}")
+                print("[case]", tag, flush=True)
+                buf = torch.full((bh * sq * d + 2 + 64,), 12.5, device=dev)
+                out = buf[1:1 + bh * sq * d]
+                fa.attention_device(variant, tq[1:].data_ptr(), tk[1:].data_ptr(), tv[1:].data_ptr(), 1, bh, sq, sk,
+                                    d, causal, out.data_ptr(), torch.cuda.current_stream().cuda_stream, path=path,
+                                    num_splits=splits)
+                torch.cuda.synchronize()
+                host = buf.cpu().numpy()
+                assert host[0] == 12.5 and np.all(host[1 + bh * sq * d:] == 12.5), "write outside out: " + tag
+                assert_parity(host[1:1 + bh * sq * d], want, tag)
+
+
 def test_two_block_workgroups_match_oracle():
     """f32 v3 grids whose block pairs fill whole rounds of the GPU run query
     blocks nqb-1-r and r in one workgroup, the second block's loads issued
