@@ -135,6 +135,7 @@ PROBES = (
     ("bf16_mfma_16x16x32", 2, 5000, PEAK_TFLOPS_16, "TFLOP/s"),
     ("bf16_mfma_32x32x16", 4, 5000, PEAK_TFLOPS_16, "TFLOP/s"),
     ("hbm_copy", 3, 0, PEAK_GBS, "GB/s"),
+    ("hbm_read", 5, 0, PEAK_GBS, "GB/s"),
 )
 PROBE_COPY_BYTES = 2 << 30   # 1 GiB copied onto another 1 GiB
 
@@ -142,7 +143,8 @@ PROBE_COPY_BYTES = 2 << 30   # 1 GiB copied onto another 1 GiB
 def measure_peaks(torch, fa) -> dict:
     """The machine's own ceilings next to the data-sheet peaks the roofline
     divides by: back-to-back MFMA streams on every CU (FLOP per launch from
-    fa_probe_launch) and a 1 GiB device copy (bytes read + written), each the best of 5 launches after a clock ramp, timed with HIP
+    fa_probe_launch), a 1 GiB device copy (bytes read + written) and a 1 GiB
+    read-only stream, each the best of 5 launches after a clock ramp, timed with HIP
     events on the launch stream."""
     stream = torch.cuda.current_stream()
     buf = torch.empty(PROBE_COPY_BYTES // 4, dtype=torch.float32, device="cuda")

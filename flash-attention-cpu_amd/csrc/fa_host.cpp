@@ -1342,8 +1342,11 @@ int fa_describe_launch(int variant, size_t batch, size_t heads, size_t sq, size_
 }
 
 int fa_probe_launch(int kind, void* stream, void* buf, size_t bytes, unsigned iters, double* work) {
-    if (kind < FA_PROBE_MFMA_F32_32X32X2 || kind > FA_PROBE_MFMA_BF16_32X32X16 || !buf || !work) return FA_ERR_INVALID_ARG;
+    if (kind < FA_PROBE_MFMA_F32_32X32X2 || kind > FA_PROBE_READ || !buf || !work) return FA_ERR_INVALID_ARG;
     if ((reinterpret_cast<uintptr_t>(buf) & 15u) != 0) return FA_ERR_INVALID_ARG;
+    const bool stream_probe = kind == FA_PROBE_COPY || kind == FA_PROBE_READ;
+    // argument checks that need no device come first
+    if (stream_probe ? bytes / 32 == 0 : iters == 0) return FA_ERR_INVALID_ARG;
     int dev;
     int rc = current_device(&dev);
     if (rc != FA_OK) return rc;
@@ -1351,20 +1354,19 @@ int fa_probe_launch(int kind, void* stream, void* buf, size_t bytes, unsigned it
     if (rc != FA_OK) return rc;
     static const char* const names[] = {"fa_probe_mfma_f32_32x32x2", "fa_probe_mfma_f32_16x16x4",
                                         "fa_probe_mfma_bf16_16x16x32", "fa_probe_copy",
-                                        "fa_probe_mfma_bf16_32x32x16"};
+                                        "fa_probe_mfma_bf16_32x32x16", "fa_probe_read"};
     const unsigned cus = static_cast<unsigned>(g_dev[dev].num_cus);
     ProbeParams pp{static_cast<float*>(buf), 0, iters};
     unsigned gx;
-    if (kind == FA_PROBE_COPY) {
-        // two halves of whole 16-byte elements: source, then destination
+    if (stream_probe) {
+        // the first half of the buffer in whole 16-byte elements: the copy's
+        // source (its destination is the second half), or the read's data
         pp.n16 = bytes / 32;
-        if (pp.n16 == 0) return FA_ERR_INVALID_ARG;
         gx = 4 * cus;
-        *work = 32.0 * (double)pp.n16;   // bytes read + bytes written
+        *work = (kind == FA_PROBE_COPY ? 32.0 : 16.0) * (double)pp.n16;   // bytes read (+ written)
     } else {
         // eight 4-wave workgroups per CU, two resident at a time; one
         // checksum float per wave
-        if (iters == 0) return FA_ERR_INVALID_ARG;
         gx = 8 * cus;
         if (bytes < (size_t)gx * 4 * sizeof(float)) return FA_ERR_INVALID_ARG;
         // FLOP per MFMA x independent chains per wave (index 3 is the copy)

@@ -391,12 +391,14 @@ PROBE_MFMA_F32_16X16X4 = 1
 PROBE_MFMA_BF16_16X16X32 = 2
 PROBE_COPY = 3
 PROBE_MFMA_BF16_32X32X16 = 4
+PROBE_READ = 5
 
 
 def probe_launch(kind: int, stream: int, buf: int, nbytes: int, iters: int = 0) -> float:
     """Queue one peak-probe kernel (fa_probe_launch) on `stream` over device
     memory `buf` (`nbytes` long); returns its work: FLOP for the MFMA probes,
-    bytes read + written for the copy.  The caller times it."""
+    bytes read + written for the copy, bytes read for the read stream.  The
+    caller times it."""
     work = ctypes.c_double(0.0)
     _check(lib().fa_probe_launch(int(kind), ctypes.c_void_p(stream), ctypes.c_void_p(buf), int(nbytes),
                                  int(iters), ctypes.byref(work)))

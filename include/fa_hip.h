@@ -288,12 +288,16 @@ int fa_describe_launch(int variant, size_t batch, size_t heads, size_t seq_len_q
  *     *work = FLOP.
  *   FA_PROBE_COPY: copies the first bytes/2 of buf (whole 16-byte elements)
  *     onto the second half;
+ *   FA_PROBE_READ: reads the first bytes/2 of buf (whole 16-byte elements),
+ *     each workgroup one contiguous chunk, and writes nothing; *work = bytes
+ *     read;
  *     *work = bytes read + bytes written. */
 #define FA_PROBE_MFMA_F32_32X32X2 0
 #define FA_PROBE_MFMA_F32_16X16X4 1
 #define FA_PROBE_MFMA_BF16_16X16X32 2
 #define FA_PROBE_COPY 3
 #define FA_PROBE_MFMA_BF16_32X32X16 4
+#define FA_PROBE_READ 5
 int fa_probe_launch(int kind, void* stream, void* buf, size_t bytes, unsigned iters, double* work);
 
 #ifdef __cplusplus

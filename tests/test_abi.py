@@ -376,7 +376,7 @@ def test_device_entry_rejects_bad_variant_without_touching_device():
 
 def test_probe_launch_rejects_bad_arguments_without_touching_device():
     # argument checks come before any device or code-object access
-    for kind, buf, nbytes in ((-1, 16, 1 << 20), (5, 16, 1 << 20), (0, 0, 1 << 20), (3, 8, 1 << 20)):
+    for kind, buf, nbytes in ((-1, 16, 1 << 20), (6, 16, 1 << 20), (0, 0, 1 << 20), (3, 8, 1 << 20), (5, 16, 16)):
         with pytest.raises(fa.FaError) as e:
             fa.probe_launch(kind, 0, buf, nbytes, 10)
         assert e.value.status == fa.FA_ERR_INVALID_ARG

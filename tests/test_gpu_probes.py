@@ -42,6 +42,17 @@ def test_copy_probe_copies_every_element():
         assert np.all(got[2 * half:] == -1.0), "wrote past the destination half"
 
 
+def test_read_probe_reads_and_writes_nothing():
+    torch = _torch()
+    nbytes = (64 << 20) + 96
+    buf = torch.rand(nbytes // 4 + 8, dtype=torch.float32, device="cuda")
+    before = buf.cpu().numpy()
+    work = fa.probe_launch(fa.PROBE_READ, torch.cuda.current_stream().cuda_stream, buf.data_ptr(), nbytes)
+    torch.cuda.synchronize()
+    assert work == 16.0 * (nbytes // 32)
+    assert np.array_equal(buf.cpu().numpy(), before), "the read stream wrote to the buffer"
+
+
 @pytest.mark.parametrize("kind", [fa.PROBE_MFMA_F32_32X32X2, fa.PROBE_MFMA_F32_16X16X4, fa.PROBE_MFMA_BF16_16X16X32,
                                   fa.PROBE_MFMA_BF16_32X32X16])
 def test_mfma_probe_checksums(kind):
