@@ -1341,12 +1341,15 @@ int fa_describe_launch(int variant, size_t batch, size_t heads, size_t sq, size_
     return rc;
 }
 
+constexpr unsigned kProbeMaxIters = 1u << 20;
+
 int fa_probe_launch(int kind, void* stream, void* buf, size_t bytes, unsigned iters, double* work) {
     if (kind < FA_PROBE_MFMA_F32_32X32X2 || kind > FA_PROBE_READ || !buf || !work) return FA_ERR_INVALID_ARG;
     if ((reinterpret_cast<uintptr_t>(buf) & 15u) != 0) return FA_ERR_INVALID_ARG;
     const bool stream_probe = kind == FA_PROBE_COPY || kind == FA_PROBE_READ;
     // argument checks that need no device come first
-    if (stream_probe ? bytes / 32 == 0 : iters == 0) return FA_ERR_INVALID_ARG;
+    // (an MFMA probe takes about a millisecond per 1,000 iterations: the cap keeps a launch near a second)
+    if (stream_probe ? bytes / 32 == 0 : (iters == 0 || iters > kProbeMaxIters)) return FA_ERR_INVALID_ARG;
     int dev;
     int rc = current_device(&dev);
     if (rc != FA_OK) return rc;

@@ -399,6 +399,8 @@ def probe_launch(kind: int, stream: int, buf: int, nbytes: int, iters: int = 0) 
     memory `buf` (`nbytes` long); returns its work: FLOP for the MFMA probes,
     bytes read + written for the copy, bytes read for the read stream.  The
     caller times it."""
+    if not 0 <= int(iters) < 1 << 32:
+        raise FaError(FA_ERR_INVALID_ARG, "iters must fit 32 bits")
     work = ctypes.c_double(0.0)
     _check(lib().fa_probe_launch(int(kind), ctypes.c_void_p(stream), ctypes.c_void_p(buf), int(nbytes),
                                  int(iters), ctypes.byref(work)))

@@ -283,9 +283,9 @@ int fa_describe_launch(int variant, size_t batch, size_t heads, size_t seq_len_q
  * machine.  Queues one probe kernel on `stream` (device memory `buf`, 16-byte
  * aligned, `bytes` long) and stores its work in *work; the caller times it.
  *   FA_PROBE_MFMA_*: every wave of 8 x #CUs four-wave workgroups (two
- *     resident per CU) runs independent chains of `iters` back-to-back MFMAs
- *     of that kind and writes one checksum float to buf (bytes >= 128 x #CUs);
- *     *work = FLOP.
+ *     resident per CU) runs independent chains of `iters` (1 .. 2^20)
+ *     back-to-back MFMAs of that kind and writes one checksum float to buf
+ *     (bytes >= 128 x #CUs); *work = FLOP.
  *   FA_PROBE_COPY: copies the first bytes/2 of buf (whole 16-byte elements)
  *     onto the second half;
  *   FA_PROBE_READ: reads the first bytes/2 of buf (whole 16-byte elements),

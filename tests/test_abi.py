@@ -380,6 +380,10 @@ def test_probe_launch_rejects_bad_arguments_without_touching_device():
         with pytest.raises(fa.FaError) as e:
             fa.probe_launch(kind, 0, buf, nbytes, 10)
         assert e.value.status == fa.FA_ERR_INVALID_ARG
+    for iters in (0, (1 << 20) + 1, -1):   # MFMA probes: 1 .. 2^20 iterations
+        with pytest.raises(fa.FaError) as e:
+            fa.probe_launch(fa.PROBE_MFMA_F32_16X16X4, 0, 16, 1 << 20, iters)
+        assert e.value.status == fa.FA_ERR_INVALID_ARG
 
 
 def test_cpp_mirror_header_compiles(tmp_path):
