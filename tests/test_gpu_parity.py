@@ -862,6 +862,30 @@ def test_explicit_softmax_scale_extension():
         assert max_abs_diff(got, want) < 1e-5
 
 
+def test_explicit_softmax_scale_on_every_split_path():
+    """The explicit scale reaches every kernel and merge: prefill, key split,
+    stream split (register-order tiles merged by fa_merge_tiles at D = 64, 128,
+    256; rows by fa_merge at D = 32) and split-KV tiles, every variant, against
+    float64 attention on Q * (s * sqrt(d)) (the same attention)."""
+    rng = np.random.default_rng(89)
+    for bh, sq, sk, d, causal, scale in ((2, 300, 500, 64, True, 0.3), (1, 200, 700, 128, False, 0.05),
+                                         (1, 260, 260, 256, True, 0.02), (2, 100, 400, 32, True, 0.5)):
+        q = rng.standard_normal(bh * sq * d, dtype=np.float32)
+        k = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        v = rng.standard_normal(bh * sk * d, dtype=np.float32)
+        q2 = (q.astype(np.float64) * scale * np.sqrt(d)).astype(np.float32)
+        want = np.concatenate([attention_f64(q2[h * sq * d:(h + 1) * sq * d], k[h * sk * d:(h + 1) * sk * d],
+                                             v[h * sk * d:(h + 1) * sk * d], sq, sk, d, causal) for h in range(bh)])
+        for path, splits in ((fa.PATH_PREFILL, 0), (fa.PATH_PREFILL, 3), (fa.PATH_STREAM, 0), (fa.PATH_SPLITKV, 2)):
+            for variant in ALL_VARIANTS:
+                tag = (f"scale {scale} v{variant} path={path} splits={splits} {bh},{sq},{sk},{d},{causal}: "
+                       f"{fa.describe_launch(variant, 1, bh, sq, sk, d, causal, path, splits)}")
+                print("[case]", tag, flush=True)
+                got = _device_run(variant, q, k, v, bh, sq, sk, d, causal, path, splits, scale=scale, guard=64)
+                err = max_abs_diff(got, want)
+                assert err < 2e-5, f"{tag}: max-abs {err:.3g}"
+
+
 def test_long_context_config3_properties():
     # 8 heads x 16384^2 causal: full parity against the CPU v2 on a sample of
     # rows (float64 naive per row) plus the causal row-0 known answer.
