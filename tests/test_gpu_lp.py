@@ -23,7 +23,7 @@ import pytest
 
 import flash_attention_amd as fa
 import oracle
-from fa_testutil import long_row_f16_case, max_abs_diff, normal_vec, rel_l2, uniform_vec
+from fa_testutil import attention_f64, long_row_f16_case, max_abs_diff, normal_vec, rel_l2, uniform_vec
 
 pytestmark = pytest.mark.gpu
 
@@ -56,7 +56,8 @@ def to16(x32: np.ndarray, dtype: int):
     return h, h.astype(np.float32)
 
 
-def lp_device(dtype, q16, k16, v16, bh, sq, sk, d, causal, path=fa.PATH_AUTO, splits=0, guard=64, misalign=False):
+def lp_device(dtype, q16, k16, v16, bh, sq, sk, d, causal, path=fa.PATH_AUTO, splits=0, guard=64, misalign=False,
+              scale=None):
     """fa_device_lp on copies of the 16-bit inputs; sentinels around O."""
     torch = _torch()
     dev = torch.device("cuda", 0)
@@ -73,7 +74,7 @@ def lp_device(dtype, q16, k16, v16, bh, sq, sk, d, causal, path=fa.PATH_AUTO, sp
     buf = torch.full((bh * sq * d + 2 * guard,), 12.5, device=dev)
     out = buf[guard:guard + bh * sq * d]
     fa.attention_device_lp(dtype, pq, pk, pv, 1, bh, sq, sk, d, causal, out.data_ptr(),
-                           torch.cuda.current_stream().cuda_stream, path=path, num_splits=splits)
+                           torch.cuda.current_stream().cuda_stream, softmax_scale=scale, path=path, num_splits=splits)
     torch.cuda.synchronize()
     host = buf.cpu().numpy()
     assert np.all(host[:guard] == 12.5) and np.all(host[-guard:] == 12.5), "write outside out"
@@ -87,6 +88,34 @@ def assert_lp(got, want, v32, dtype, what):
     print(f"[lp-parity] {what}: max-abs {ma:.3g} (bound {tol:.3g}) rel-L2 {rl:.3g} (bound {u:.3g})", flush=True)
     assert ma <= tol, (what, ma, tol)
     assert rl <= u, (what, rl, u)
+
+
+@pytest.mark.parametrize("dtype", [fa.DTYPE_BF16, fa.DTYPE_F16])
+def test_lp_explicit_softmax_scale_on_every_path(dtype):
+    """The explicit scale through the 16-bit prefill, its key split and
+    stream split (D = 128) and the split-KV kernels (rows and tiles), against
+    float64 attention on the widened inputs with Q * (s * sqrt(d)), under the
+    derived bound."""
+    rng = np.random.default_rng(97)
+    A, P, K, S, T, R = fa.PATH_AUTO, fa.PATH_PREFILL, fa.PATH_PREFILL, fa.PATH_STREAM, fa.PATH_SPLITKV, fa.PATH_SPLITKV_ROWS
+    cases = [((2, 300, 500, 64, True, 0.3), [(A, 0), (P, 0), (K, 3)]),
+             ((1, 200, 700, 128, False, 0.05), [(A, 0), (P, 0), (K, 3), (S, 0)]),
+             ((1, 130, 260, 256, True, 0.02), [(A, 0), (P, 0), (K, 2)]),
+             ((4, 1, 3000, 128, False, 0.2), [(A, 0), (T, 4), (R, 4)]),
+             ((2, 16, 1500, 64, False, 0.4), [(A, 0), (T, 3)])]
+    for (bh, sq, sk, d, causal, scale), paths in cases:
+        q16, q32 = to16(rng.standard_normal(bh * sq * d, dtype=np.float32), dtype)
+        k16, k32 = to16(rng.standard_normal(bh * sk * d, dtype=np.float32), dtype)
+        v16, v32 = to16(rng.standard_normal(bh * sk * d, dtype=np.float32), dtype)
+        qs = q32.astype(np.float64) * scale * np.sqrt(d)   # exact in float64
+        want = np.concatenate([attention_f64(qs[h * sq * d:(h + 1) * sq * d], k32[h * sk * d:(h + 1) * sk * d],
+                                             v32[h * sk * d:(h + 1) * sk * d], sq, sk, d, causal) for h in range(bh)])
+        for path, splits in paths:
+            what = (f"{NAME[dtype]} scale {scale} path={path} splits={splits} {bh}x{sq}x{sk} d={d} causal={causal}: "
+                    f"{fa.describe_launch(3, 1, bh, sq, sk, d, causal, path, splits, dtype)}")
+            print("[case]", what, flush=True)
+            got = lp_device(dtype, q16, k16, v16, bh, sq, sk, d, causal, path, splits, scale=scale)
+            assert_lp(got, want, v32, dtype, what)
 
 
 CASES = [(1, 1, 1, 8, False), (2, 64, 64, 64, False), (3, 100, 37, 128, True), (1, 37, 100, 256, False),
